@@ -1,0 +1,194 @@
+/*
+ * tmhd.h - C ABI of libtmhd.so, the gfx950 (MI355X) implementation of the
+ * TaoMate-HD streaming KV-cache attention hook and its selective W8A8
+ * projection.
+ *
+ * Every entry point takes plain device pointers, element strides and sizes,
+ * plus the HIP stream (passed as void*) the work is ordered on.  The library
+ * never allocates or frees device memory: scratch buffers are arguments.
+ * Every entry point returns a tmhd_status; 0 means the work was enqueued.
+ * tmhd_last_error() returns a message for the calling thread's last failure.
+ *
+ * Storage formats owned by this library
+ * -------------------------------------
+ *  Slot (one KV-cache block of one layer, "head-major"):
+ *    k  : bf16 [H][cap][D]   row t of head h at k + h*k_head_stride + t*D
+ *    vt : bf16 [H][D][cap]   value (h, t, d) at vt + h*vt_head_stride
+ *                            + d*vt_row_stride + tmhd_vt_position(t)
+ *    cap is a multiple of 64; rows in [tokens, round_up(tokens, 64)) are zero.
+ *  tmhd_vt_position(t) swaps the middle two 4-token chunks of every 16-token
+ *  group ((t & ~15) | perm[(t >> 2) & 3] << 2 | (t & 3), perm = {0,2,1,3}).
+ *  This puts the 8 tokens one MFMA lane consumes for P.V next to each other.
+ *
+ *  Token-major tensors ([T][H][D], the hook's q/k/v/o) are addressed as
+ *  base + row*token_stride + h*head_stride + d, with an optional int32 row
+ *  list selecting rows.
+ */
+#ifndef TMHD_H
+#define TMHD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TMHD_MAX_SEGMENTS 8
+#define TMHD_KV_TILE 64
+#define TMHD_QUANT_BLOCK 128
+
+typedef enum tmhd_status {
+  TMHD_OK = 0,
+  TMHD_ERR_INVALID = 1,     /* bad pointer, shape, stride or alignment */
+  TMHD_ERR_UNSUPPORTED = 2, /* valid but not implemented (e.g. head_dim) */
+  TMHD_ERR_HIP = 3          /* a HIP launch failed */
+} tmhd_status;
+
+/* One key/value segment of an attention call, stored in slot format. */
+typedef struct tmhd_kv_segment {
+  const void *k;          /* bf16 slot keys */
+  const void *vt;         /* bf16 slot values, transposed and interleaved */
+  int64_t k_head_stride;  /* elements between heads of k (>= cap*D) */
+  int64_t vt_head_stride; /* elements between heads of vt (>= D*cap) */
+  int32_t vt_row_stride;  /* elements between d rows of vt (= cap) */
+  int32_t tokens;         /* valid tokens, 0 < tokens <= cap */
+} tmhd_kv_segment;
+
+/* softmax(q k^T * scale) v over the concatenation of the segments; no mask. */
+typedef struct tmhd_attn_args {
+  const void *q;          /* bf16 token-major queries */
+  int64_t q_token_stride; /* elements */
+  int64_t q_head_stride;  /* elements */
+  const int32_t *q_rows;  /* device row list of length lq, or NULL */
+  int32_t q_row0;         /* first row when q_rows is NULL */
+  int32_t lq;             /* query rows */
+  void *o;                /* bf16 token-major output */
+  int64_t o_token_stride;
+  int64_t o_head_stride;
+  const int32_t *o_rows;  /* device row list of length lq, or NULL */
+  int32_t o_row0;
+  int32_t heads;
+  int32_t head_dim;       /* 64 or 128 */
+  float scale;            /* softmax scale (head_dim ** -0.5 in the model) */
+  int32_t n_segments;     /* 1..TMHD_MAX_SEGMENTS */
+  tmhd_kv_segment seg[TMHD_MAX_SEGMENTS];
+} tmhd_attn_args;
+
+/*
+ * Quantized operands of the INT8-QK attention (SageAttention-style).
+ *   k_mean[h][d]   = bf16 mean of all keys of the call (all segments)
+ *   Q block b of head h: rows [128b, 128b+128) of the call's queries
+ *   K block b of segment s, head h: tokens [128b, 128b+128) of the segment
+ *   scale = amax / 127, value = sat_int8(rint(x * (127 / amax))), amax = 0 -> 0
+ *   with x = q for Q and x = k - k_mean for K (fp32).
+ */
+typedef struct tmhd_qk_quant {
+  int8_t *q_i8;                 /* [H][q_cap][D], q_cap >= round_up(lq, 256) */
+  float *q_scale;               /* [H][q_cap / 128] */
+  int64_t q_head_stride;        /* elements of q_i8 between heads */
+  int32_t q_scale_head_stride;  /* elements of q_scale between heads */
+  int32_t reserved0;
+  int8_t *k_i8[TMHD_MAX_SEGMENTS];      /* [H][cap][D] per segment */
+  float *k_scale[TMHD_MAX_SEGMENTS];    /* [H][cap / 128] per segment */
+  int64_t k_head_stride[TMHD_MAX_SEGMENTS];       /* elements */
+  int32_t k_scale_head_stride[TMHD_MAX_SEGMENTS]; /* elements */
+  uint16_t *k_mean;             /* bf16 [H][D] written by tmhd_qk_smooth_quant */
+  int64_t *mean_workspace;      /* int64 [H][D] scratch */
+} tmhd_qk_quant;
+
+/* Library identification: "tmhd <version> gfx950". */
+const char *tmhd_version(void);
+/* Message of the calling thread's last non-zero status ("" if none). */
+const char *tmhd_last_error(void);
+
+/*
+ * BF16 streaming attention (serial-mode SDPA semantics).
+ * Replaces torch SDPA in _sdpa_from_kv_parts,
+ * src/taomate_hd/streaming/attention_hook.py:100-115, including the dense
+ * K/V materialisation of _materialize_dense_kv_parts (:56-97): the segments
+ * are read in place.
+ */
+int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream);
+
+/*
+ * INT8-QK streaming attention: int8 Q.K^T (int32 accumulate) dequantised by
+ * the per-block scales, fp32 online softmax, bf16 P.V with fp32 accumulate.
+ * Replaces sageattn_qk_int8_pv_fp8_cuda_sm90 / sage_with_fused_value_padding,
+ * src/taomate_hd/streaming/attention_hook.py:335-371 and
+ * src/taomate_hd/inference/sage_value_padding.py:79-97.
+ * The operands must have been produced by tmhd_qk_smooth_quant.
+ */
+int tmhd_attn_fwd_i8qk(const tmhd_attn_args *args, const tmhd_qk_quant *quant,
+                       void *stream);
+
+/*
+ * K token-mean over every segment, then per-128-block INT8 quantization of
+ * Q and of K - mean (formula above).  Replaces the k.mean(dim=1) and
+ * per_thread_int8_triton step of
+ * src/taomate_hd/inference/sage_value_padding.py:89-92.
+ */
+int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_quant *quant,
+                         void *stream);
+
+/*
+ * Copy `n` token-major K/V rows into a slot at token offset `dst`, then zero
+ * slot rows [dst + n, zero_to).  Source row i is rows[i] (or row0 + i).
+ * Replaces the index_select staging and torch.cat commit of
+ * src/taomate_hd/streaming/cache.py:273-296 and the dense copies of
+ * src/taomate_hd/streaming/attention_hook.py:71-91.
+ */
+int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride,
+                 int64_t head_stride, const int32_t *rows, int32_t row0,
+                 int32_t n, void *k_slot, void *vt_slot, int64_t k_head_stride,
+                 int64_t vt_head_stride, int32_t vt_row_stride, int32_t dst,
+                 int32_t zero_to, int32_t heads, int32_t head_dim, void *stream);
+
+/*
+ * Per-token dynamic symmetric INT8 quantization of a bf16 [rows][cols]
+ * matrix (row stride x_stride elements): scale[m] = amax_m / 127,
+ * q[m][k] = sat_int8(rint(x[m][k] * (127 / amax_m))), amax_m = 0 -> 0.
+ * Replaces vLLM dynamic_scaled_int8_quant / scaled_int8_quant called at
+ * src/taomate_hd/inference/w8a8.py:71 and :141.
+ */
+int tmhd_token_quant_i8(int8_t *q, float *scale, const void *x, int32_t rows,
+                        int32_t cols, int64_t x_stride, void *stream);
+
+/*
+ * Static per-output-channel INT8 weight quantization of a bf16 [n][k]
+ * weight: scale[r] = max(amax_r / 127, 1e-12),
+ * q[r][c] = clamp(rint(w[r][c] / scale[r]), -127, 127).
+ * Replaces _quantize_cutlass_w8a8_weight, src/taomate_hd/inference/w8a8.py:175-179.
+ */
+int tmhd_weight_quant_i8(int8_t *q, float *scale, const void *w, int32_t n,
+                         int32_t k, void *stream);
+
+/*
+ * Scaled INT8 GEMM with a bf16 epilogue:
+ *   acc[m][n] = sum_k a[m][k] * b[n][k]                  (exact int32)
+ *   out[m][n] = bf16(float(acc) * b_scale[n] * a_scale[m] + bias[n])
+ * evaluated in fp32 in that order (bias term skipped when bias is NULL).
+ * a is row-major [m][k] (stride lda), b is the row-major [n][k] weight
+ * (stride ldb), i.e. the [k][n] column-major operand of cutlass_scaled_mm.
+ * Replaces vLLM cutlass_scaled_mm called at
+ * src/taomate_hd/inference/w8a8.py:72 and :142-144.
+ * k must be a multiple of 64; a, b rows 16-byte aligned.
+ */
+int tmhd_gemm_w8a8(void *out, const int8_t *a, const int8_t *b,
+                   const float *a_scale, const float *b_scale,
+                   const void *bias, int32_t m, int32_t n, int32_t k,
+                   int64_t lda, int64_t ldb, int64_t ldo, void *stream);
+
+/*
+ * The same GEMM writing the raw int32 accumulators (no scales, no bias).
+ * No counterpart in the reference: it exposes the accumulators that
+ * cutlass_scaled_mm keeps internal, for exactness checks.
+ */
+int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m,
+                     int32_t n, int32_t k, int64_t lda, int64_t ldb,
+                     int64_t ldo, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMHD_H */

@@ -1,0 +1,427 @@
+// Streaming attention forward for gfx950: softmax(q k^T * scale) v over a
+// table of key/value segments held in slot format (see tmhd.h), no mask.
+//
+// Reference semantics: torch SDPA over the concatenated K/V parts in
+// src/taomate_hd/streaming/attention_hook.py:100-115 (BF16 path) and the
+// SageAttention call at :335-371 (INT8-QK path).  Attention without a mask is
+// invariant to the order of keys, so segments are visited in place in table
+// order and never concatenated.
+//
+// Work decomposition
+//   workgroup = 4 waves = 256 query rows of one head; each wave owns 64 rows
+//   (two 32-row MFMA column blocks) and keeps them, their fp32 output
+//   accumulators and the online-softmax state in registers (1 wave per SIMD).
+//   Keys stream through LDS in 64-token tiles, double-buffered: the next
+//   tile's global loads are in flight while the current tile is computed.
+//   Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16
+//   (or v_mfma_i32_32x32x32_i8), so each lane holds 16 keys of one query
+//   column; the same registers, converted to bf16, are directly the B operand
+//   of O^T += V^T P^T.  The value slot layout (transposed, 4-token chunks
+//   interleaved) makes the matching A operand one 16-byte LDS read.
+//   Online softmax works in log2 units with a lazy rescale: the running max
+//   is only moved (and O, l rescaled) when a tile exceeds it by 2^8.
+#include <math.h>
+
+#include "tmhd_internal.h"
+
+namespace tmhd {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kQW = 64;            // query rows per wave
+constexpr int kBM = kWaves * kQW;  // query rows per workgroup
+constexpr int kBN = 64;            // keys per tile
+constexpr float kLazyRescale = 8.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct Seg {
+  const uint16_t *k;
+  const uint16_t *vt;
+  const int8_t *k8;
+  const float *ks;
+  int64_t khs;
+  int64_t vhs;
+  int32_t vrs;
+  int32_t tokens;
+  int32_t kshs;
+  int32_t ntiles;
+};
+
+struct KArgs {
+  const uint16_t *q;
+  int64_t qts, qhs;
+  const int32_t *q_rows;
+  int32_t q_row0, lq;
+  uint16_t *o;
+  int64_t ots, ohs;
+  const int32_t *o_rows;
+  int32_t o_row0;
+  const int8_t *q8;
+  const float *qs;
+  int64_t q8hs;
+  int32_t qshs;
+  int32_t heads, nqt;
+  float c;  // softmax scale * log2(e)
+  int32_t nseg;
+  Seg seg[kMaxSeg];
+};
+
+__device__ __forceinline__ f32x16 mfma_bf16(i32x4 a, i32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Maps the linear workgroup id so that consecutive logical ids run on the same
+// XCD (the hardware deals workgroups round-robin over the 8 XCDs).  Logical
+// ids are head-major, so the workgroups that share one head's keys and values
+// share that XCD's L2.
+__device__ __forceinline__ int xcd_logical_id(int b, int G) {
+  const int xcd = b & 7, pos = b >> 3, per = G >> 3, rem = G & 7;
+  return xcd < rem ? xcd * (per + 1) + pos : rem * (per + 1) + (xcd - rem) * per + pos;
+}
+
+template <int D, bool I8>
+__global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const KArgs a) {
+  constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row
+  constexpr int KCPR = KROW / 16;       // 16-byte chunks per key row
+  constexpr int KSW = (KCPR < 8 ? KCPR : 8) - 1;
+  constexpr int KT = kBN * KROW;        // key tile bytes
+  constexpr int VT = D * kBN * 2;       // value tile bytes (D rows of 64 keys)
+  constexpr int KLD = KT / (16 * 256);  // 16-byte loads per thread per tile
+  constexpr int VLD = VT / (16 * 256);
+  constexpr int QST = I8 ? D / 32 : D / 16;  // MFMA k-steps over head_dim
+  constexpr int DB = D / 32;
+  static_assert(KLD >= 1 && VLD >= 1, "tile too small for 256 threads");
+
+  __shared__ __attribute__((aligned(16))) char smem[2 * (KT + VT)];
+
+  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int h = L / a.nqt;
+  const int qt = L - h * a.nqt;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
+
+  // ---- query operands (B operand of S^T = K Q^T), resident for the whole call
+  i32x4 qv[2][QST];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int ql = qt * kBM + w * kQW + qb * 32 + lr;
+    if (ql < a.lq) {
+      if constexpr (I8) {
+        const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
+#pragma unroll
+        for (int st = 0; st < QST; ++st) qv[qb][st] = *(const i32x4 *)(p + st * 32);
+      } else {
+        const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
+        const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
+#pragma unroll
+        for (int st = 0; st < QST; ++st) qv[qb][st] = *(const i32x4 *)(p + st * 16);
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < QST; ++st) qv[qb][st] = i32x4{0, 0, 0, 0};
+    }
+  }
+  float qscale = 1.0f;
+  if constexpr (I8) qscale = a.qs[(int64_t)h * a.qshs + (qt * kBM + w * kQW) / TMHD_QUANT_BLOCK];
+
+  f32x16 o[2][DB];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.0f;
+  float mref[2] = {-INFINITY, -INFINITY};
+  float lsum[2] = {0.0f, 0.0f};
+
+  i32x4 kreg[KLD], vreg[VLD];
+  auto gload = [&](int s, int t) {
+    const Seg &S = a.seg[s];
+    const int t0 = t * kBN;
+    if constexpr (I8) {
+      const int8_t *kb = S.k8 + (int64_t)h * S.khs + (int64_t)t0 * D;
+#pragma unroll
+      for (int i = 0; i < KLD; ++i) {
+        const int c = i * 256 + tid, row = c / KCPR, ch = (c % KCPR) ^ (row & KSW);
+        kreg[i] = *(const i32x4 *)(kb + row * D + ch * 16);
+      }
+    } else {
+      const uint16_t *kb = S.k + (int64_t)h * S.khs + (int64_t)t0 * D;
+#pragma unroll
+      for (int i = 0; i < KLD; ++i) {
+        const int c = i * 256 + tid, row = c / KCPR, ch = (c % KCPR) ^ (row & KSW);
+        kreg[i] = *(const i32x4 *)(kb + row * D + ch * 8);
+      }
+    }
+    const uint16_t *vb = S.vt + (int64_t)h * S.vhs + t0;
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) {
+      const int c = i * 256 + tid, row = c >> 3, ch = (c & 7) ^ (row & 7);
+      vreg[i] = *(const i32x4 *)(vb + (int64_t)row * S.vrs + ch * 8);
+    }
+  };
+  auto lstore = [&](int buf) {
+    char *kb = smem + buf * (KT + VT);
+    char *vb = kb + KT;
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) *(i32x4 *)(kb + (i * 256 + tid) * 16) = kreg[i];
+#pragma unroll
+    for (int i = 0; i < VLD; ++i) *(i32x4 *)(vb + (i * 256 + tid) * 16) = vreg[i];
+  };
+
+  auto compute = [&](int buf, int s, int t) {
+    const Seg &S = a.seg[s];
+    const char *kb = smem + buf * (KT + VT);
+    const char *vb = kb + KT;
+    const int nvalid = S.tokens - t * kBN;
+    float ct = a.c;
+    if constexpr (I8) ct = a.c * qscale * S.ks[(int64_t)h * S.kshs + (t * kBN) / TMHD_QUANT_BLOCK];
+#pragma unroll
+    for (int kb32 = 0; kb32 < 2; ++kb32) {
+      if (kb32 * 32 >= nvalid) break;
+      const int krow = kb32 * 32 + lr;
+      f32x16 sc[2];
+      if constexpr (I8) {
+        i32x16 ia[2];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ia[0][r] = ia[1][r] = 0;
+#pragma unroll
+        for (int st = 0; st < QST; ++st) {
+          const i32x4 kk = *(const i32x4 *)(kb + (krow * KCPR + ((2 * st + g) ^ (krow & KSW))) * 16);
+          ia[0] = mfma_i8(kk, qv[0][st], ia[0]);
+          ia[1] = mfma_i8(kk, qv[1][st], ia[1]);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sc[0][r] = (float)ia[0][r];
+          sc[1][r] = (float)ia[1][r];
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[0][r] = sc[1][r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < QST; ++st) {
+          const i32x4 kk = *(const i32x4 *)(kb + (krow * KCPR + ((2 * st + g) ^ (krow & KSW))) * 16);
+          sc[0] = mfma_bf16(kk, qv[0][st], sc[0]);
+          sc[1] = mfma_bf16(kk, qv[1][st], sc[1]);
+        }
+      }
+      // keys of this lane: kb32*32 + 8*(r/4) + 4*g + r%4
+      const int rem = nvalid - kb32 * 32;
+      const bool partial = rem < 32;
+      float cand[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float m = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const bool ok = !partial || (8 * (r >> 2) + 4 * g + (r & 3)) < rem;
+          m = ok ? fmaxf(m, sc[qb][r]) : m;
+        }
+        m = fmaxf(m, __shfl_xor(m, 32));
+        cand[qb] = m * ct;
+      }
+      const bool need = (cand[0] > mref[0] + kLazyRescale) || (cand[1] > mref[1] + kLazyRescale);
+      if (__any(need)) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const float mn = fmaxf(mref[qb], cand[qb]);
+          const float alpha = (mref[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mref[qb] - mn);
+          lsum[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+          mref[qb] = mn;
+        }
+      }
+      uint32_t pk[2][8];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float nm = -mref[qb];
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          float p0 = __builtin_amdgcn_exp2f(fmaf(sc[qb][r], ct, nm));
+          float p1 = __builtin_amdgcn_exp2f(fmaf(sc[qb][r + 1], ct, nm));
+          if (partial) {
+            p0 = (8 * (r >> 2) + 4 * g + (r & 3)) < rem ? p0 : 0.0f;
+            p1 = (8 * ((r + 1) >> 2) + 4 * g + ((r + 1) & 3)) < rem ? p1 : 0.0f;
+          }
+          pk[qb][r >> 1] = pack_bf16x2(p0, p1);
+        }
+        float ls = lsum[qb];
+        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[qb][i]), ones, ls, false);
+        lsum[qb] = ls;
+      }
+      // O^T += V^T P^T over the 32 keys of this block (two 16-key steps)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        const int vrow = db * 32 + lr;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const i32x4 vv = *(const i32x4 *)(vb + (vrow * 8 + ((4 * kb32 + 2 * st + g) ^ (vrow & 7))) * 16);
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            const i32x4 pb = {(int)pk[qb][4 * st], (int)pk[qb][4 * st + 1], (int)pk[qb][4 * st + 2],
+                              (int)pk[qb][4 * st + 3]};
+            o[qb][db] = mfma_bf16(vv, pb, o[qb][db]);
+          }
+        }
+      }
+    }
+  };
+
+  // ---- key/value tile loop over the segment table
+  int s = 0, t = 0;
+  gload(s, t);
+  lstore(0);
+  __syncthreads();
+  int buf = 0;
+  for (;;) {
+    int ns = s, nt = t + 1;
+    if (nt >= a.seg[s].ntiles) {
+      ns = s + 1;
+      nt = 0;
+    }
+    const bool has_next = ns < a.nseg;
+    if (has_next) gload(ns, nt);
+    compute(buf, s, t);
+    if (!has_next) break;
+    lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+    s = ns;
+    t = nt;
+  }
+
+  // ---- epilogue: O = O^T / l, written token-major
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float lt = lsum[qb] + __shfl_xor(lsum[qb], 32);
+    const float inv = 1.0f / lt;
+    const int ql = qt * kBM + w * kQW + qb * 32 + lr;
+    if (ql < a.lq) {
+      const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
+      uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const f32x16 &v = o[qb][db];
+          i32x2 pr = {(int)pack_bf16x2(v[4 * u] * inv, v[4 * u + 1] * inv),
+                      (int)pack_bf16x2(v[4 * u + 2] * inv, v[4 * u + 3] * inv)};
+          *(i32x2 *)(op + db * 32 + 8 * u) = pr;
+        }
+    }
+  }
+}
+
+bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+int build_kargs(const tmhd_attn_args *args, const tmhd_qk_quant *qq, bool i8, KArgs *k) {
+  if (!args) return set_error(TMHD_ERR_INVALID, "attention: null args");
+  const int D = args->head_dim;
+  if (D != 64 && D != 128) return set_error(TMHD_ERR_UNSUPPORTED, "attention: head_dim %d (64 or 128)", D);
+  if (args->heads <= 0 || args->lq < 0) return set_error(TMHD_ERR_INVALID, "attention: heads %d lq %d", args->heads, args->lq);
+  if (args->n_segments < 1 || args->n_segments > kMaxSeg)
+    return set_error(TMHD_ERR_INVALID, "attention: n_segments %d not in [1, %d]", args->n_segments, kMaxSeg);
+  if (!(args->scale > 0.0f) || !isfinite(args->scale)) return set_error(TMHD_ERR_INVALID, "attention: scale must be > 0");
+  if (!args->o || !aligned(args->o, 8) || args->o_token_stride % 4 || args->o_head_stride % 4)
+    return set_error(TMHD_ERR_INVALID, "attention: output pointer/strides must be 8-byte aligned");
+  if (!i8 && (!args->q || !aligned(args->q, 16) || args->q_token_stride % 8 || args->q_head_stride % 8))
+    return set_error(TMHD_ERR_INVALID, "attention: query pointer/strides must be 16-byte aligned");
+  const int nqt = (args->lq + kBM - 1) / kBM;
+  *k = KArgs{};
+  k->q = (const uint16_t *)args->q;
+  k->qts = args->q_token_stride;
+  k->qhs = args->q_head_stride;
+  k->q_rows = args->q_rows;
+  k->q_row0 = args->q_row0;
+  k->lq = args->lq;
+  k->o = (uint16_t *)args->o;
+  k->ots = args->o_token_stride;
+  k->ohs = args->o_head_stride;
+  k->o_rows = args->o_rows;
+  k->o_row0 = args->o_row0;
+  k->heads = args->heads;
+  k->nqt = nqt;
+  k->c = args->scale * kLog2e;
+  k->nseg = args->n_segments;
+  if (i8) {
+    if (!qq || !qq->q_i8 || !qq->q_scale || !aligned(qq->q_i8, 16) || qq->q_head_stride % 16)
+      return set_error(TMHD_ERR_INVALID, "attention i8: bad quantized query buffers");
+    if (qq->q_head_stride < (int64_t)nqt * kBM * D || qq->q_scale_head_stride < nqt * (kBM / TMHD_QUANT_BLOCK))
+      return set_error(TMHD_ERR_INVALID, "attention i8: quantized query capacity below round_up(lq, 256)");
+    k->q8 = qq->q_i8;
+    k->qs = qq->q_scale;
+    k->q8hs = qq->q_head_stride;
+    k->qshs = qq->q_scale_head_stride;
+  }
+  for (int i = 0; i < args->n_segments; ++i) {
+    const tmhd_kv_segment &sg = args->seg[i];
+    const int64_t cap = ((int64_t)sg.tokens + kBN - 1) / kBN * kBN;
+    if (sg.tokens <= 0) return set_error(TMHD_ERR_INVALID, "attention: segment %d has %d tokens", i, sg.tokens);
+    if (!sg.k || !sg.vt || !aligned(sg.k, 16) || !aligned(sg.vt, 16))
+      return set_error(TMHD_ERR_INVALID, "attention: segment %d pointers must be 16-byte aligned", i);
+    if (sg.vt_row_stride % kBN || sg.vt_row_stride < cap || sg.vt_head_stride < (int64_t)D * sg.vt_row_stride ||
+        sg.k_head_stride < cap * D || sg.vt_head_stride % 8 || sg.k_head_stride % 8)
+      return set_error(TMHD_ERR_INVALID,
+                       "attention: segment %d is not a slot (tokens %d, vt_row_stride %d, strides %lld/%lld)", i,
+                       sg.tokens, sg.vt_row_stride, (long long)sg.k_head_stride, (long long)sg.vt_head_stride);
+    Seg &S = k->seg[i];
+    S.k = (const uint16_t *)sg.k;
+    S.vt = (const uint16_t *)sg.vt;
+    S.khs = sg.k_head_stride;
+    S.vhs = sg.vt_head_stride;
+    S.vrs = sg.vt_row_stride;
+    S.tokens = sg.tokens;
+    S.ntiles = (int)(cap / kBN);
+    if (i8) {
+      if (!qq->k_i8[i] || !qq->k_scale[i] || !aligned(qq->k_i8[i], 16) || qq->k_head_stride[i] < cap * D ||
+          qq->k_head_stride[i] % 16 || qq->k_scale_head_stride[i] < (cap + TMHD_QUANT_BLOCK - 1) / TMHD_QUANT_BLOCK)
+        return set_error(TMHD_ERR_INVALID, "attention i8: bad quantized key buffers for segment %d", i);
+      S.k8 = qq->k_i8[i];
+      S.ks = qq->k_scale[i];
+      S.khs = qq->k_head_stride[i];
+      S.kshs = qq->k_scale_head_stride[i];
+    }
+  }
+  return TMHD_OK;
+}
+
+template <bool I8>
+int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *stream) {
+  KArgs k;
+  int st = build_kargs(args, qq, I8, &k);
+  if (st) return st;
+  if (args->lq == 0) return TMHD_OK;
+  const int64_t grid = (int64_t)k.nqt * k.heads;
+  if (grid > 0x7fffffff) return set_error(TMHD_ERR_UNSUPPORTED, "attention: grid too large");
+  hipStream_t s = (hipStream_t)stream;
+  if (args->head_dim == 128)
+    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3((unsigned)grid), dim3(256), 0, s, k);
+  else
+    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3((unsigned)grid), dim3(256), 0, s, k);
+  return check_launch(I8 ? "tmhd_attn_fwd_i8qk" : "tmhd_attn_fwd_bf16");
+}
+
+}  // namespace
+}  // namespace tmhd
+
+extern "C" int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream) {
+  return tmhd::launch_attn<false>(args, nullptr, stream);
+}
+
+extern "C" int tmhd_attn_fwd_i8qk(const tmhd_attn_args *args, const tmhd_qk_quant *quant, void *stream) {
+  return tmhd::launch_attn<true>(args, quant, stream);
+}

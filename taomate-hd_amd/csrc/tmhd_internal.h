@@ -1,0 +1,65 @@
+// Internal helpers shared by the libtmhd HIP sources (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tmhd.h"
+
+namespace tmhd {
+
+using i32x2 = int __attribute__((ext_vector_type(2)));
+using i32x4 = int __attribute__((ext_vector_type(4)));
+using i32x16 = int __attribute__((ext_vector_type(16)));
+using f32x4 = float __attribute__((ext_vector_type(4)));
+using f32x16 = float __attribute__((ext_vector_type(16)));
+using bf16x2 = __bf16 __attribute__((ext_vector_type(2)));
+using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
+
+// Records a formatted message for tmhd_last_error() and returns `status`.
+int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Checks hipGetLastError() after a launch; records it on failure.
+int check_launch(const char *what);
+
+// bf16 bits -> fp32 (exact).
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  uint32_t u = __float_as_uint(f);
+#else
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+#endif
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Slot position of token t inside the transposed value rows: swap the middle
+// two 4-token chunks of each 16-token group (an involution).
+__host__ __device__ __forceinline__ int vt_position(int t) {
+  const int c = (t >> 2) & 3;
+  const int pc = (c == 1) ? 2 : (c == 2) ? 1 : c;
+  return (t & ~15) | (pc << 2) | (t & 3);
+}
+
+// Saturating round-to-nearest-even fp32 -> int8.
+__device__ __forceinline__ int quant_rne_sat(float x) {
+  float r = __builtin_rintf(x);
+  r = fminf(fmaxf(r, -128.0f), 127.0f);
+  return (int)r;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+constexpr int kMaxSeg = TMHD_MAX_SEGMENTS;
+
+}  // namespace tmhd

@@ -1,0 +1,292 @@
+// Slot packing (token-major K/V rows -> head-major slot) and the smooth-K
+// INT8 quantization of the INT8-QK attention path.
+#include <math.h>
+
+#include "tmhd_internal.h"
+
+namespace tmhd {
+namespace {
+
+constexpr int kTile = 64;
+
+// ---------------------------------------------------------------------------
+// tmhd_kv_pack: one workgroup = 64 slot positions of one head.
+// Position p of the slot is: data row (p - dst) if dst <= p < dst + n,
+// zero if dst + n <= p < zero_to, untouched otherwise.
+template <int D>
+__global__ void __launch_bounds__(256) kv_pack_kernel(const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+                                                      int64_t ts, int64_t hs, const int32_t *__restrict__ rows,
+                                                      int32_t row0, int32_t n, uint16_t *__restrict__ ks,
+                                                      uint16_t *__restrict__ vts, int64_t khs, int64_t vhs, int32_t vrs,
+                                                      int32_t dst, int32_t zero_to, int32_t p_begin) {
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  __shared__ uint16_t tile[kTile][D + 2];
+  const int h = blockIdx.y;
+  const int p0 = p_begin + blockIdx.x * kTile;
+  const int tid = threadIdx.x;
+  auto cls = [&](int p) -> int {  // 0 untouched, 1 data, 2 zero
+    if (p >= dst && p < dst + n) return 1;
+    if (p >= dst + n && p < zero_to) return 2;
+    return 0;
+  };
+  // keys: direct row copies; values: staged in LDS for the transpose
+  for (int c = tid; c < kTile * CPR; c += 256) {
+    const int r = c / CPR, ch = c % CPR, p = p0 + r;
+    const int kind = cls(p);
+    i32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+    if (kind == 1) {
+      const int i = p - dst;
+      const int64_t src = (int64_t)(rows ? rows[i] : row0 + i) * ts + (int64_t)h * hs + ch * 8;
+      kv = *(const i32x4 *)(k + src);
+      vv = *(const i32x4 *)(v + src);
+    }
+    if (kind != 0) *(i32x4 *)(ks + (int64_t)h * khs + (int64_t)p * D + ch * 8) = kv;
+    const uint32_t *vw = (const uint32_t *)&vv;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[r][ch * 8 + 2 * e] = (uint16_t)(vw[e] & 0xffffu);
+      tile[r][ch * 8 + 2 * e + 1] = (uint16_t)(vw[e] >> 16);
+    }
+  }
+  __syncthreads();
+  // transposed values: D rows of 64 positions = 8 chunks of 8 positions each
+  for (int c = tid; c < D * 8; c += 256) {
+    const int d = c >> 3, ch = c & 7;
+    uint16_t vals[8];
+    int nwrite = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = vt_position(ch * 8 + e);  // token held at this stored position
+      vals[e] = tile[tok][d];
+      nwrite += cls(p0 + tok) != 0;
+    }
+    uint16_t *out = vts + (int64_t)h * vhs + (int64_t)d * vrs + p0 + ch * 8;
+    if (nwrite == 8) {
+      i32x4 pk;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) pk[e] = (int)((uint32_t)vals[2 * e] | ((uint32_t)vals[2 * e + 1] << 16));
+      *(i32x4 *)out = pk;
+    } else if (nwrite > 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (cls(p0 + vt_position(ch * 8 + e)) != 0) out[e] = vals[e];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Smooth-K mean.  Keys are summed exactly as int64 fixed point (x * 2^24,
+// rounded to nearest even), so the sum does not depend on the order of the
+// parallel reduction; mean = bf16(fp32(sum * 2^-24 / N)).
+constexpr double kMeanFix = 16777216.0;  // 2^24
+
+__global__ void zero_i64_kernel(int64_t *p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+__device__ __forceinline__ int64_t to_fixed(float x) {
+  float y = x * 16777216.0f;
+  y = fminf(fmaxf(y, -4.0e18f), 4.0e18f);
+  return (int64_t)__builtin_rintf(y);
+}
+
+// grid (ceil(tokens / 1024), H); thread (d = tid % D, part = tid / D)
+template <int D>
+__global__ void __launch_bounds__(256) k_sum_kernel(const uint16_t *__restrict__ k, int64_t khs, int32_t tokens,
+                                                    int64_t *__restrict__ ws) {
+  constexpr int PARTS = 256 / D;
+  __shared__ long long part_sum[256];
+  const int h = blockIdx.y, tid = threadIdx.x, d = tid % D, part = tid / D;
+  const int t0 = blockIdx.x * 1024;
+  const int t1 = min(t0 + 1024, tokens);
+  const uint16_t *base = k + (int64_t)h * khs + d;
+  long long acc = 0;
+  for (int t = t0 + part; t < t1; t += PARTS) acc += to_fixed(bf16_bits_to_f32(base[(int64_t)t * D]));
+  part_sum[tid] = acc;
+  __syncthreads();
+  if (part == 0) {
+    for (int p = 1; p < PARTS; ++p) acc += part_sum[p * D + d];
+    atomicAdd((unsigned long long *)(ws + h * D + d), (unsigned long long)acc);
+  }
+}
+
+__global__ void k_mean_finalize_kernel(const int64_t *__restrict__ ws, uint16_t *__restrict__ mean, int n,
+                                       double count) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    const double m = __ddiv_rn((double)ws[i], count * kMeanFix);
+    mean[i] = f32_to_bf16_bits((float)m);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per-(head, 128-row block) symmetric INT8 quantization of x = src - mean:
+//   amax = max |x| over the block's valid rows, scale = amax / 127,
+//   q = sat_int8(rint(x * (127 / amax))) (amax = 0: scale 0, q 0).
+// Rows in [nvalid, nwrite) are written as zero; every launched block writes
+// its scale (0 for a block without valid rows).
+template <int D>
+__global__ void __launch_bounds__(256) block_quant_kernel(const uint16_t *__restrict__ src, int64_t sts, int64_t shs,
+                                                          const int32_t *__restrict__ rows, int32_t row0,
+                                                          const uint16_t *__restrict__ mean, int32_t nvalid,
+                                                          int32_t nwrite, int8_t *__restrict__ q8, int64_t q8hs,
+                                                          float *__restrict__ qscale, int32_t qshs) {
+  constexpr int CPR = D / 8;          // 8-element chunks per row
+  constexpr int RPI = 256 / CPR;      // rows per pass
+  constexpr int NP = TMHD_QUANT_BLOCK / RPI;
+  __shared__ float red[4];
+  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int ch = tid % CPR, r0 = tid / CPR;
+  float mf[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) mf[e] = mean ? bf16_bits_to_f32(mean[h * D + ch * 8 + e]) : 0.0f;
+  float x[NP][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = blk * TMHD_QUANT_BLOCK + p * RPI + r0;
+    if (i < nvalid) {
+      const int row = rows ? rows[i] : row0 + i;
+      const i32x4 raw = *(const i32x4 *)(src + (int64_t)row * sts + (int64_t)h * shs + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)raw[e];
+        x[p][2 * e] = bf16_bits_to_f32(w & 0xffffu) - mf[2 * e];
+        x[p][2 * e + 1] = bf16_bits_to_f32(w >> 16) - mf[2 * e + 1];
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[p][e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[p][e] = 0.0f;
+    }
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float inv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  if (tid == 0) qscale[(int64_t)h * qshs + blk] = __fdiv_rn(amax, 127.0f);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int i = blk * TMHD_QUANT_BLOCK + p * RPI + r0;
+    if (i < nwrite) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        lo |= ((uint32_t)quant_rne_sat(x[p][e] * inv) & 0xffu) << (8 * e);
+        hi |= ((uint32_t)quant_rne_sat(x[p][4 + e] * inv) & 0xffu) << (8 * e);
+      }
+      *(i32x2 *)(q8 + (int64_t)h * q8hs + (int64_t)i * D + ch * 8) = i32x2{(int)lo, (int)hi};
+    }
+  }
+}
+
+bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+template <int D>
+int launch_block_quant(const uint16_t *src, int64_t sts, int64_t shs, const int32_t *rows, int32_t row0,
+                       const uint16_t *mean, int32_t nvalid, int32_t nwrite, int8_t *q8, int64_t q8hs, float *qs,
+                       int32_t qshs, int heads, hipStream_t s) {
+  const int nblk = (nwrite + TMHD_QUANT_BLOCK - 1) / TMHD_QUANT_BLOCK;
+  if (nblk == 0) return TMHD_OK;
+  hipLaunchKernelGGL(block_quant_kernel<D>, dim3(nblk, heads), dim3(256), 0, s, src, sts, shs, rows, row0, mean,
+                     nvalid, nwrite, q8, q8hs, qs, qshs);
+  return check_launch("block_quant");
+}
+
+template <int D>
+int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s) {
+  const int H = a->heads;
+  int64_t total = 0;
+  for (int i = 0; i < a->n_segments; ++i) total += a->seg[i].tokens;
+  // 1. exact key sums, 2. bf16 mean
+  hipLaunchKernelGGL(zero_i64_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, H * D);
+  for (int i = 0; i < a->n_segments; ++i) {
+    const tmhd_kv_segment &sg = a->seg[i];
+    hipLaunchKernelGGL(k_sum_kernel<D>, dim3((sg.tokens + 1023) / 1024, H), dim3(256), 0, s,
+                       (const uint16_t *)sg.k, sg.k_head_stride, sg.tokens, qq->mean_workspace);
+  }
+  hipLaunchKernelGGL(k_mean_finalize_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace,
+                     qq->k_mean, H * D, (double)total);
+  if (int st = check_launch("smooth-K mean")) return st;
+  // 3. keys, per segment (rows up to the 64-token tile padding are written)
+  for (int i = 0; i < a->n_segments; ++i) {
+    const tmhd_kv_segment &sg = a->seg[i];
+    const int nwrite = (sg.tokens + kTile - 1) / kTile * kTile;
+    if (int st = launch_block_quant<D>((const uint16_t *)sg.k, D, sg.k_head_stride, nullptr, 0, qq->k_mean,
+                                       sg.tokens, nwrite, qq->k_i8[i], qq->k_head_stride[i], qq->k_scale[i],
+                                       qq->k_scale_head_stride[i], H, s))
+      return st;
+  }
+  // 4. queries (rows up to the 256-row workgroup padding are written)
+  const int qcap = (a->lq + 255) / 256 * 256;
+  return launch_block_quant<D>((const uint16_t *)a->q, a->q_token_stride, a->q_head_stride, a->q_rows, a->q_row0,
+                               nullptr, a->lq, qcap, qq->q_i8, qq->q_head_stride, qq->q_scale,
+                               qq->q_scale_head_stride, H, s);
+}
+
+}  // namespace
+}  // namespace tmhd
+
+extern "C" int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_stride,
+                            const int32_t *rows, int32_t row0, int32_t n, void *k_slot, void *vt_slot,
+                            int64_t k_head_stride, int64_t vt_head_stride, int32_t vt_row_stride, int32_t dst,
+                            int32_t zero_to, int32_t heads, int32_t head_dim, void *stream) {
+  using namespace tmhd;
+  if (head_dim != 64 && head_dim != 128) return set_error(TMHD_ERR_UNSUPPORTED, "kv_pack: head_dim %d", head_dim);
+  if (n < 0 || dst < 0 || heads <= 0) return set_error(TMHD_ERR_INVALID, "kv_pack: n %d dst %d heads %d", n, dst, heads);
+  const int end = max(dst + n, zero_to);
+  const int p_begin = dst / kTile * kTile;
+  const int p_end = (end + kTile - 1) / kTile * kTile;
+  if (p_end > vt_row_stride || vt_row_stride % kTile || (int64_t)vt_row_stride * head_dim > vt_head_stride ||
+      (int64_t)p_end * head_dim > k_head_stride)
+    return set_error(TMHD_ERR_INVALID, "kv_pack: positions [%d, %d) exceed the slot (cap %d)", p_begin, p_end,
+                     vt_row_stride);
+  if ((n > 0 && (!k || !v)) || !k_slot || !vt_slot || !aligned(k_slot, 16) || !aligned(vt_slot, 16) ||
+      (n > 0 && (!aligned(k, 16) || !aligned(v, 16))) || token_stride % 8 || head_stride % 8 || k_head_stride % 8 ||
+      vt_head_stride % 8)
+    return set_error(TMHD_ERR_INVALID, "kv_pack: pointers and strides must be 16-byte aligned");
+  if (p_end == p_begin) return TMHD_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((p_end - p_begin) / kTile, heads);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(kv_pack_kernel<128>, grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v,
+                       token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,
+                       k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin);
+  else
+    hipLaunchKernelGGL(kv_pack_kernel<64>, grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v,
+                       token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,
+                       k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin);
+  return check_launch("tmhd_kv_pack");
+}
+
+extern "C" int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_quant *quant, void *stream) {
+  using namespace tmhd;
+  if (!args || !quant) return set_error(TMHD_ERR_INVALID, "smooth_quant: null arguments");
+  const int D = args->head_dim;
+  if (D != 64 && D != 128) return set_error(TMHD_ERR_UNSUPPORTED, "smooth_quant: head_dim %d", D);
+  if (args->n_segments < 1 || args->n_segments > kMaxSeg || args->heads <= 0 || args->lq < 0)
+    return set_error(TMHD_ERR_INVALID, "smooth_quant: bad segment count / heads / lq");
+  if (!quant->k_mean || !quant->mean_workspace || !quant->q_i8 || !quant->q_scale)
+    return set_error(TMHD_ERR_INVALID, "smooth_quant: null output buffers");
+  const int qcap = (args->lq + 255) / 256 * 256;
+  if (quant->q_head_stride < (int64_t)qcap * D || quant->q_scale_head_stride < qcap / TMHD_QUANT_BLOCK ||
+      !aligned(quant->q_i8, 16) || quant->q_head_stride % 16)
+    return set_error(TMHD_ERR_INVALID, "smooth_quant: quantized query buffer below round_up(lq, 256) rows");
+  if (args->lq > 0 && (!args->q || !aligned(args->q, 16) || args->q_token_stride % 8 || args->q_head_stride % 8))
+    return set_error(TMHD_ERR_INVALID, "smooth_quant: query pointer/strides must be 16-byte aligned");
+  for (int i = 0; i < args->n_segments; ++i) {
+    const tmhd_kv_segment &sg = args->seg[i];
+    const int64_t cap = ((int64_t)sg.tokens + kTile - 1) / kTile * kTile;
+    if (sg.tokens <= 0 || !sg.k || !aligned(sg.k, 16) || sg.k_head_stride < cap * D || sg.k_head_stride % 8)
+      return set_error(TMHD_ERR_INVALID, "smooth_quant: segment %d keys are not a slot", i);
+    if (!quant->k_i8[i] || !quant->k_scale[i] || !aligned(quant->k_i8[i], 16) || quant->k_head_stride[i] < cap * D ||
+        quant->k_head_stride[i] % 16 ||
+        quant->k_scale_head_stride[i] < (sg.tokens + TMHD_QUANT_BLOCK - 1) / TMHD_QUANT_BLOCK)
+      return set_error(TMHD_ERR_INVALID, "smooth_quant: segment %d quantized key buffers too small", i);
+  }
+  hipStream_t s = (hipStream_t)stream;
+  return D == 128 ? smooth_quant<128>(args, quant, s) : smooth_quant<64>(args, quant, s);
+}

@@ -1,0 +1,302 @@
+// Selective W8A8 projection for gfx950: per-token dynamic INT8 activation
+// quantization, per-output-channel INT8 weight quantization and the scaled
+// INT8 GEMM with a bf16 epilogue (reference call sites:
+// src/taomate_hd/inference/w8a8.py:67-73, 117-145, 175-179).
+#include <math.h>
+
+#include "tmhd_internal.h"
+
+namespace tmhd {
+namespace {
+
+// ---------------------------------------------------------------------------
+// Row quantization, one wave per row.  CH = 8-element chunks held per lane
+// (one pass, row kept in registers); CH = 0 streams the row twice.
+// WEIGHT selects the weight formula of _quantize_cutlass_w8a8_weight:
+//   scale = max(amax / 127, 1e-12), q = clamp(rint(w / scale), -127, 127)
+// otherwise the activation formula:
+//   scale = amax / 127, q = sat_int8(rint(x * (127 / amax))), amax = 0 -> 0.
+template <int CH, bool WEIGHT>
+__global__ void __launch_bounds__(256) row_quant_kernel(int8_t *__restrict__ q, float *__restrict__ scale,
+                                                        const uint16_t *__restrict__ x, int32_t rows, int32_t cols,
+                                                        int64_t xs) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int nch = cols >> 3;
+  const uint16_t *xr = x + (int64_t)row * xs;
+  int8_t *qr = q + (int64_t)row * cols;
+  float amax = 0.0f;
+  i32x4 raw[CH > 0 ? CH : 1];
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      raw[j] = c < nch ? *(const i32x4 *)(xr + c * 8) : i32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)raw[j][e];
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_bits_to_f32(w & 0xffffu)), fabsf(bf16_bits_to_f32(w >> 16))));
+      }
+    }
+  } else {
+    for (int c = lane; c < nch; c += 64) {
+      const i32x4 r = *(const i32x4 *)(xr + c * 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = (uint32_t)r[e];
+        amax = fmaxf(amax, fmaxf(fabsf(bf16_bits_to_f32(w & 0xffffu)), fabsf(bf16_bits_to_f32(w >> 16))));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  float sc, inv;
+  if constexpr (WEIGHT) {
+    sc = fmaxf(__fdiv_rn(amax, 127.0f), 1e-12f);
+    inv = 0.0f;
+  } else {
+    sc = __fdiv_rn(amax, 127.0f);
+    inv = amax > 0.0f ? __fdiv_rn(127.0f, amax) : 0.0f;
+  }
+  if (lane == 0) scale[row] = sc;
+  auto qv = [&](float v) -> uint32_t {
+    int r;
+    if constexpr (WEIGHT) {
+      r = (int)fminf(fmaxf(__builtin_rintf(__fdiv_rn(v, sc)), -127.0f), 127.0f);
+    } else {
+      r = quant_rne_sat(v * inv);
+    }
+    return (uint32_t)r & 0xffu;
+  };
+  auto emit = [&](int c, i32x4 r) {
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const uint32_t w0 = (uint32_t)r[e], w1 = (uint32_t)r[e + 2];
+      lo |= qv(bf16_bits_to_f32(w0 & 0xffffu)) << (16 * e);
+      lo |= qv(bf16_bits_to_f32(w0 >> 16)) << (16 * e + 8);
+      hi |= qv(bf16_bits_to_f32(w1 & 0xffffu)) << (16 * e);
+      hi |= qv(bf16_bits_to_f32(w1 >> 16)) << (16 * e + 8);
+    }
+    *(i32x2 *)(qr + c * 8) = i32x2{(int)lo, (int)hi};
+  };
+  if constexpr (CH > 0) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < nch) emit(c, raw[j]);
+    }
+  } else {
+    for (int c = lane; c < nch; c += 64) emit(c, *(const i32x4 *)(xr + c * 8));
+  }
+}
+
+template <bool WEIGHT>
+int launch_row_quant(int8_t *q, float *scale, const void *x, int32_t rows, int32_t cols, int64_t xs, void *stream,
+                     const char *what) {
+  if (rows < 0 || cols <= 0 || cols % 8) return set_error(TMHD_ERR_UNSUPPORTED, "%s: cols %d must be a positive multiple of 8", what, cols);
+  if (xs < cols || xs % 8) return set_error(TMHD_ERR_INVALID, "%s: row stride %lld", what, (long long)xs);
+  if (!q || !scale || !x || ((uintptr_t)x % 16) || ((uintptr_t)q % 8))
+    return set_error(TMHD_ERR_INVALID, "%s: null or misaligned pointer", what);
+  if (rows == 0) return TMHD_OK;
+  const int need = (cols / 8 + 63) / 64;
+  const dim3 grid((rows + 3) / 4), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  const uint16_t *xp = (const uint16_t *)x;
+  if (need <= 1)
+    hipLaunchKernelGGL((row_quant_kernel<1, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else if (need <= 2)
+    hipLaunchKernelGGL((row_quant_kernel<2, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else if (need <= 4)
+    hipLaunchKernelGGL((row_quant_kernel<4, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else if (need <= 8)
+    hipLaunchKernelGGL((row_quant_kernel<8, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else if (need <= 10)
+    hipLaunchKernelGGL((row_quant_kernel<10, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else if (need <= 16)
+    hipLaunchKernelGGL((row_quant_kernel<16, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  else
+    hipLaunchKernelGGL((row_quant_kernel<0, WEIGHT>), grid, block, 0, s, q, scale, xp, rows, cols, xs);
+  return check_launch(what);
+}
+
+// ---------------------------------------------------------------------------
+// INT8 GEMM: C[m][n] = sum_k A[m][k] * B[n][k] with v_mfma_i32_32x32x32_i8.
+// Workgroup tile 256 x 256 (4 waves of 128 x 128), k-tile 64, double-buffered
+// LDS.  LDS rows are 64 bytes (4 chunks of 16); chunk c of row r is stored at
+// c ^ ((r >> 1) & 3) so the 8 lanes of one ds_read_b128 phase hit 8 distinct
+// 16-byte bank groups.
+constexpr int GBM = 256, GBN = 256, GBK = 64;
+
+struct GArgs {
+  const int8_t *a;
+  const int8_t *b;
+  void *out;
+  const float *as;
+  const float *bs;
+  const uint16_t *bias;
+  int32_t m, n, k;
+  int64_t lda, ldb, ldo;
+  int32_t tm_count, tn_count;
+};
+
+__device__ __forceinline__ int xcd_logical_id(int b, int G) {
+  const int xcd = b & 7, pos = b >> 3, per = G >> 3, rem = G & 7;
+  return xcd < rem ? xcd * (per + 1) + pos : rem * (per + 1) + (xcd - rem) * per + pos;
+}
+
+template <bool RAW>
+__global__ void __launch_bounds__(256, 1) gemm_i8_kernel(const GArgs ga) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) char smem[2 * (GBM + GBN) * GBK];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
+  const int wm = w >> 1, wn = w & 1;
+  // grouped tile order: 8 row tiles share each column sweep (L2 reuse)
+  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * ga.tn_count;
+  const int grp = L / per_group;
+  const int first_tm = grp * GROUP;
+  const int gsize = min(ga.tm_count - first_tm, GROUP);
+  const int tm = first_tm + (L % per_group) % gsize;
+  const int tn = (L % per_group) / gsize;
+  const int m0 = tm * GBM, n0 = tn * GBN;
+
+  i32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  i32x4 ra[4], rb[4];
+  const int8_t *arow[4];
+  const int8_t *brow[4];
+  int lpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = i * 256 + tid, row = c >> 2, ch = c & 3;
+    arow[i] = ga.a + (int64_t)min(m0 + row, ga.m - 1) * ga.lda + ch * 16;
+    brow[i] = ga.b + (int64_t)min(n0 + row, ga.n - 1) * ga.ldb + ch * 16;
+    lpos[i] = (row * 4 + (ch ^ ((row >> 1) & 3))) * 16;
+  }
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ra[i] = *(const i32x4 *)(arow[i] + k0);
+      rb[i] = *(const i32x4 *)(brow[i] + k0);
+    }
+  };
+  auto lstore = [&](int buf) {
+    char *sa = smem + buf * (GBM + GBN) * GBK;
+    char *sb = sa + GBM * GBK;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(i32x4 *)(sa + lpos[i]) = ra[i];
+      *(i32x4 *)(sb + lpos[i]) = rb[i];
+    }
+  };
+  auto compute = [&](int buf) {
+    const char *sa = smem + buf * (GBM + GBN) * GBK;
+    const char *sb = sa + GBM * GBK;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      i32x4 av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ar = wm * 128 + i * 32 + lr, br = wn * 128 + i * 32 + lr;
+        av[i] = *(const i32x4 *)(sa + (ar * 4 + ((2 * ks + g) ^ ((ar >> 1) & 3))) * 16);
+        bv[i] = *(const i32x4 *)(sb + (br * 4 + ((2 * ks + g) ^ ((br >> 1) & 3))) * 16);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int nk = ga.k / GBK;
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  int buf = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    const bool has_next = kt + 1 < nk;
+    if (has_next) gload((kt + 1) * GBK);
+    compute(buf);
+    if (!has_next) break;
+    lstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // epilogue: lane holds column n = lr of each 32x32 block, rows 8*(r/4)+4*g+r%4
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + wn * 128 + j * 32 + lr;
+    if (n >= ga.n) continue;
+    float bsn = 0.0f, biasn = 0.0f;
+    if constexpr (!RAW) {
+      bsn = ga.bs[n];
+      if (ga.bias) biasn = bf16_bits_to_f32(ga.bias[n]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (m < ga.m) {
+          if constexpr (RAW) {
+            ((int32_t *)ga.out)[(int64_t)m * ga.ldo + n] = acc[i][j][r];
+          } else {
+            float t = (float)acc[i][j][r];
+            t = t * bsn;
+            t = t * ga.as[m];
+            if (ga.bias) t = t + biasn;
+            ((uint16_t *)ga.out)[(int64_t)m * ga.ldo + n] = f32_to_bf16_bits(t);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <bool RAW>
+int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, const float *bs, const void *bias,
+                int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *stream) {
+  const char *what = RAW ? "tmhd_gemm_i8_i32" : "tmhd_gemm_w8a8";
+  if (m < 0 || n <= 0 || k <= 0) return set_error(TMHD_ERR_INVALID, "%s: m %d n %d k %d", what, m, n, k);
+  if (k % GBK) return set_error(TMHD_ERR_UNSUPPORTED, "%s: k %d must be a multiple of %d", what, k, GBK);
+  if (!out || !a || !b || (!RAW && (!as || !bs))) return set_error(TMHD_ERR_INVALID, "%s: null pointer", what);
+  if (((uintptr_t)a % 16) || ((uintptr_t)b % 16) || lda % 16 || ldb % 16 || lda < k || ldb < k || ldo < n)
+    return set_error(TMHD_ERR_INVALID, "%s: operands must be 16-byte aligned rows with stride >= k", what);
+  if (m == 0) return TMHD_OK;
+  GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + GBM - 1) / GBM, (n + GBN - 1) / GBN};
+  const int64_t grid = (int64_t)ga.tm_count * ga.tn_count;
+  hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, ga);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace tmhd
+
+extern "C" int tmhd_token_quant_i8(int8_t *q, float *scale, const void *x, int32_t rows, int32_t cols,
+                                   int64_t x_stride, void *stream) {
+  return tmhd::launch_row_quant<false>(q, scale, x, rows, cols, x_stride, stream, "tmhd_token_quant_i8");
+}
+
+extern "C" int tmhd_weight_quant_i8(int8_t *q, float *scale, const void *w, int32_t n, int32_t k, void *stream) {
+  return tmhd::launch_row_quant<true>(q, scale, w, n, k, k, stream, "tmhd_weight_quant_i8");
+}
+
+extern "C" int tmhd_gemm_w8a8(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
+                              const float *b_scale, const void *bias, int32_t m, int32_t n, int32_t k, int64_t lda,
+                              int64_t ldb, int64_t ldo, void *stream) {
+  return tmhd::launch_gemm<false>(out, a, b, a_scale, b_scale, bias, m, n, k, lda, ldb, ldo, stream);
+}
+
+extern "C" int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m, int32_t n, int32_t k,
+                                int64_t lda, int64_t ldb, int64_t ldo, void *stream) {
+  return tmhd::launch_gemm<true>(out, a, b, nullptr, nullptr, nullptr, m, n, k, lda, ldb, ldo, stream);
+}

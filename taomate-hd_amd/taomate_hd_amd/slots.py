@@ -1,0 +1,156 @@
+"""Head-major K/V slots: the storage unit of the streaming KV cache.
+
+A slot holds one block of keys and values for one layer:
+
+* ``k``  bf16 ``[H, cap, D]``  - key row ``t`` of head ``h`` is ``k[h, t]``;
+* ``vt`` bf16 ``[H, D, cap]``  - values transposed; token ``t`` sits at column
+  ``vt_position(t)`` (the middle two 4-token chunks of every 16-token group
+  swapped), which is the order one MFMA lane consumes in ``P . V``.
+
+``cap`` is a multiple of 64 (the kernels' key tile) and rows ``[tokens,
+round_up(tokens, 64))`` are kept zero, so a tile never reads stale data.
+Slots are filled only by ``tmhd_kv_pack``; attention reads them in place.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any
+
+from . import _native
+
+KV_TILE = _native.KV_TILE
+
+
+def round_up(value: int, multiple: int) -> int:
+    return (int(value) + multiple - 1) // multiple * multiple
+
+
+def vt_position(t: int) -> int:
+    """Column of token ``t`` inside a transposed value row (an involution)."""
+    chunk = (t >> 2) & 3
+    perm = (0, 2, 1, 3)[chunk]
+    return (t & ~15) | (perm << 2) | (t & 3)
+
+
+@dataclass
+class SlotView:
+    """The first ``tokens`` rows of a slot, as one attention segment."""
+
+    slot: "KVSlot"
+    tokens: int
+
+    def to_segment(self) -> _native.KVSegment:
+        s = self.slot
+        return _native.KVSegment(
+            k=_native.ptr(s.k),
+            vt=_native.ptr(s.vt),
+            k_head_stride=s.capacity * s.head_dim,
+            vt_head_stride=s.capacity * s.head_dim,
+            vt_row_stride=s.capacity,
+            tokens=int(self.tokens),
+        )
+
+
+class KVSlot:
+    """One head-major key/value block (see module docstring)."""
+
+    def __init__(self, torch: Any, *, heads: int, head_dim: int, capacity: int, device: Any) -> None:
+        self._torch = torch
+        self.heads = int(heads)
+        self.head_dim = int(head_dim)
+        self.capacity = max(KV_TILE, round_up(capacity, KV_TILE))
+        self.device = torch.device(device)
+        self.k = torch.empty((self.heads, self.capacity, self.head_dim), dtype=torch.bfloat16, device=self.device)
+        self.vt = torch.empty((self.heads, self.head_dim, self.capacity), dtype=torch.bfloat16, device=self.device)
+        self.tokens = 0
+
+    @property
+    def nbytes(self) -> int:
+        return 2 * self.k.numel() * self.k.element_size()
+
+    def view(self, tokens: int | None = None) -> SlotView:
+        count = self.tokens if tokens is None else int(tokens)
+        if not 0 < count <= self.tokens:
+            raise ValueError(f"slot view of {count} tokens outside the {self.tokens} packed rows")
+        return SlotView(self, count)
+
+    def pack(self, key: Any, value: Any, *, rows: Any | None = None, row0: int = 0, count: int | None = None) -> None:
+        """Copy token-major rows of ``key``/``value`` ([T, H, D] bf16) into the slot.
+
+        ``rows`` is an int32/int64 GPU index tensor; without it rows
+        ``row0 .. row0 + count`` are copied.
+        """
+        torch = self._torch
+        for name, t in (("key", key), ("value", value)):
+            _native.require_device_tensor(torch, t, name)
+            if t.dtype != torch.bfloat16 or t.ndim != 3 or t.stride(2) != 1:
+                raise ValueError(f"{name} must be a [tokens, heads, dim] bf16 view with unit dim stride")
+        if key.shape != value.shape or key.stride() != value.stride():
+            raise ValueError("key and value must share shape and strides")
+        if tuple(key.shape[1:]) != (self.heads, self.head_dim):
+            raise ValueError(f"K/V heads x dim {tuple(key.shape[1:])} differ from slot {(self.heads, self.head_dim)}")
+        rows_ptr = None
+        if rows is not None:
+            if rows.dtype != torch.int32:
+                rows = rows.to(torch.int32)
+            rows = rows.contiguous()
+            n = int(rows.numel())
+            rows_ptr = _native.ptr(rows) if n else None
+        else:
+            n = int(key.shape[0]) - int(row0) if count is None else int(count)
+            if int(row0) < 0 or n < 0 or int(row0) + n > int(key.shape[0]):
+                raise ValueError(f"rows [{row0}, {int(row0) + n}) outside the {int(key.shape[0])} K/V rows")
+        if n > self.capacity:
+            raise ValueError(f"{n} rows exceed the slot capacity {self.capacity}")
+        lib = _native.load()
+        status = lib.tmhd_kv_pack(
+            _native.ptr(key), _native.ptr(value), key.stride(0), key.stride(1), rows_ptr, int(row0), n,
+            _native.ptr(self.k), _native.ptr(self.vt), self.capacity * self.head_dim,
+            self.capacity * self.head_dim, self.capacity, 0, round_up(n, KV_TILE), self.heads,
+            self.head_dim, _native.stream_ptr(torch, key.device),
+        )
+        _native.check(status, "tmhd_kv_pack")
+        self.tokens = n
+
+    def token_major(self, tokens: int | None = None, order: Any | None = None) -> tuple[Any, Any]:
+        """Materialise ``[tokens, H, D]`` key/value copies (compatibility path)."""
+        torch = self._torch
+        n = self.tokens if tokens is None else int(tokens)
+        key = self.k[:, :n, :].permute(1, 0, 2).contiguous()
+        cols = torch.tensor([vt_position(t) for t in range(n)], dtype=torch.long, device=self.device)
+        value = self.vt.index_select(2, cols).permute(2, 0, 1).contiguous()
+        if order is not None:
+            key = key.index_select(0, order)
+            value = value.index_select(0, order)
+        return key, value
+
+
+class SlotPool:
+    """Grow-only pool of slots of one shape family, recycled without copies."""
+
+    def __init__(self, torch: Any, *, heads: int, head_dim: int, device: Any) -> None:
+        self._torch = torch
+        self.heads = heads
+        self.head_dim = head_dim
+        self.device = device
+        self._free: list[KVSlot] = []
+
+    def acquire(self, tokens: int) -> KVSlot:
+        need = round_up(max(int(tokens), 1), KV_TILE)
+        best = None
+        for slot in self._free:
+            if slot.capacity >= need and (best is None or slot.capacity < best.capacity):
+                best = slot
+        if best is not None:
+            self._free.remove(best)
+            best.tokens = 0
+            return best
+        return KVSlot(self._torch, heads=self.heads, head_dim=self.head_dim, capacity=need, device=self.device)
+
+    def release(self, slot: KVSlot) -> None:
+        slot.tokens = 0
+        self._free.append(slot)
+
+    def clear(self) -> None:
+        self._free.clear()

@@ -1,0 +1,231 @@
+"""Parity of the HIP kernels (called through the C ABI) against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle import bf16
+from oracle import quant as oq
+from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+# BF16 attention gate (BASELINE): max abs <= 2e-2 and mean abs <= 1e-3 vs fp32/fp64 SDPA
+BF16_MAX_ABS = 2e-2
+BF16_MEAN_ABS = 1e-3
+# INT8-QK gate: cosine >= 0.999 vs fp32 SDPA on the unquantized inputs
+I8_COSINE = 0.999
+
+
+def _slots(torch, dev, k, v, splits):
+    from taomate_hd_amd import KVSlot
+
+    views, off = [], 0
+    kd, vd = to_dev(k, dev), to_dev(v, dev)
+    for n in splits:
+        slot = KVSlot(torch, heads=k.shape[1], head_dim=k.shape[2], capacity=n, device=dev)
+        slot.pack(kd, vd, row0=off, count=n)
+        views.append(slot.view())
+        off += n
+    return views
+
+
+def test_pack_roundtrip_and_padding(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import KVSlot, vt_position
+
+    H, D, T = 3, 128, 150
+    k = randn_bf16((T, H, D), 1)
+    v = randn_bf16((T, H, D), 2)
+    kd, vd = to_dev(k, dev), to_dev(v, dev)
+    rows = torch.tensor([5, 149, 0, 77, 77, 3] + list(range(10, 100)), dtype=torch.int32, device=dev)
+    slot = KVSlot(torch, heads=H, head_dim=D, capacity=200, device=dev)
+    slot.k.fill_(7.0)
+    slot.vt.fill_(7.0)
+    slot.pack(kd, vd, rows=rows)
+    torch.cuda.synchronize()
+    sel = rows.cpu().numpy()
+    kk = bf16.from_torch(slot.k)  # [H, cap, D]
+    vt = bf16.from_torch(slot.vt)  # [H, D, cap]
+    n = len(sel)
+    assert np.array_equal(kk[:, :n, :], k[sel].transpose(1, 0, 2))
+    cols = np.array([vt_position(t) for t in range(n)])
+    assert np.array_equal(vt[:, :, cols], v[sel].transpose(1, 2, 0))
+    pad_end = (n + 63) // 64 * 64
+    assert np.all(kk[:, n:pad_end, :] == 0)
+    pad_cols = np.array([vt_position(t) for t in range(n, pad_end)])
+    assert np.all(vt[:, :, pad_cols] == 0)
+    # untouched beyond the 64-row padding
+    assert np.all(kk[:, pad_end:, :] == 7.0)
+    # range form
+    slot2 = KVSlot(torch, heads=H, head_dim=D, capacity=64, device=dev)
+    slot2.pack(kd, vd, row0=100, count=50)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(slot2.k)[:, :50, :], k[100:150].transpose(1, 0, 2))
+    key, value = slot2.token_major()
+    assert np.array_equal(bf16.from_torch(key), k[100:150])
+    assert np.array_equal(bf16.from_torch(value), v[100:150])
+
+
+ATTN_CASES = [
+    # heads, dim, lq, segment token counts
+    (8, 64, 256, [768, 256]),  # plumbing config: 768 history + 256 self
+    (2, 128, 300, [100, 37, 500]),
+    (3, 128, 513, [64, 1, 63, 129]),
+    (1, 128, 1, [5]),
+    (2, 64, 700, [1000, 333, 4, 65, 2, 128, 7, 300]),
+]
+
+
+@pytest.mark.parametrize("heads,dim,lq,splits", ATTN_CASES)
+def test_bf16_attention_matches_fp64(torch_mod, dev, heads, dim, lq, splits):
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    n = sum(splits)
+    q = randn_bf16((lq, heads, dim), 10)
+    k = randn_bf16((n, heads, dim), 11, offset=key_offset(heads, dim, 13))
+    v = randn_bf16((n, heads, dim), 12)
+    views = _slots(torch, dev, k, v, splits)
+    out = segment_attention(torch, to_dev(q, dev), views, scale=dim ** -0.5)
+    torch.cuda.synchronize()
+    got = bf16.from_torch(out)
+    want = oatt.attention_fp64(q, k, v, dim ** -0.5)
+    mx, mean = err_stats(got, want)
+    assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+
+
+def test_bf16_attention_row_gather_scatter(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    H, D, T = 4, 128, 400
+    q = randn_bf16((T, H, D), 20)
+    k = randn_bf16((T, H, D), 21)
+    v = randn_bf16((T, H, D), 22)
+    views = _slots(torch, dev, k, v, [T])
+    rng = np.random.default_rng(0)
+    rows = np.sort(rng.choice(T, size=170, replace=False))
+    qd = to_dev(q, dev)
+    # strided query view: every other token of a doubled buffer
+    qbig = torch.zeros((2 * T, H, D), dtype=torch.bfloat16, device=dev)
+    qbig[::2] = qd
+    out = torch.full((T, H, D), 3.0, dtype=torch.bfloat16, device=dev)
+    rows_d = torch.tensor(rows, dtype=torch.int32, device=dev)
+    segment_attention(torch, qbig[::2], views, scale=D ** -0.5, q_rows=rows_d, out=out, o_rows=rows_d)
+    torch.cuda.synchronize()
+    got = bf16.from_torch(out)
+    want = oatt.attention_fp64(q[rows], k, v, D ** -0.5)
+    mx, mean = err_stats(got[rows], want)
+    assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS
+    untouched = np.setdiff1d(np.arange(T), rows)
+    assert np.all(got[untouched] == 3.0)
+
+
+@pytest.mark.parametrize("heads,dim,lq,splits", [(4, 128, 600, [300, 700, 129]), (2, 64, 256, [768, 256])])
+def test_i8qk_attention(torch_mod, dev, heads, dim, lq, splits):
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    n = sum(splits)
+    q = randn_bf16((lq, heads, dim), 30)
+    k = randn_bf16((n, heads, dim), 31, offset=key_offset(heads, dim, 33))
+    v = randn_bf16((n, heads, dim), 32)
+    views = _slots(torch, dev, k, v, splits)
+    out, qv = segment_attention(
+        torch, to_dev(q, dev), views, scale=dim ** -0.5, backend="i8qk", return_quant=True
+    )
+    torch.cuda.synchronize()
+    ksegs, vsegs, off = [], [], 0
+    for s in splits:
+        ksegs.append(k[off : off + s])
+        vsegs.append(v[off : off + s])
+        off += s
+    want_q, ops = oatt.i8qk_attention(q, ksegs, vsegs, dim ** -0.5)
+    # quantized operands: bit-exact
+    assert np.array_equal(bf16.from_torch(qv["k_mean"]), ops["mean"])
+    qi8 = qv["q_i8"].cpu().numpy()  # [H, qcap, D]
+    assert np.array_equal(qi8[:, :lq, :], ops["q_i8"].transpose(1, 0, 2))
+    assert np.all(qi8[:, lq:, :] == 0)
+    nqb = ops["q_scale"].shape[1]
+    assert np.array_equal(qv["q_scale"].cpu().numpy()[:, :nqb], ops["q_scale"])
+    for i, s in enumerate(splits):
+        ki8 = qv["k_i8"][i].cpu().numpy()
+        assert np.array_equal(ki8[:, :s, :], ops["k_i8"][i].transpose(1, 0, 2))
+        assert np.array_equal(qv["k_scale"][i].cpu().numpy()[:, : ops["k_scale"][i].shape[1]], ops["k_scale"][i])
+    got = bf16.from_torch(out)
+    ref32 = oatt.attention_fp64(q, k, v, dim ** -0.5)
+    assert oatt.cosine(got, ref32) >= I8_COSINE
+    mx, mean = err_stats(got, want_q)
+    assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+
+
+def test_token_quant_bit_exact(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import quant
+
+    x = randn_bf16((77, 5120), 40)
+    x[:, 7] *= 20.0
+    x = bf16.round_f32(x)
+    x[3] = 0.0  # a zero row
+    x[5, :] = 0.0
+    x[5, 100] = -2.5
+    q, s, azp = quant.scaled_int8_quant(to_dev(x, dev))
+    torch.cuda.synchronize()
+    assert azp is None
+    wq, ws = oq.token_quant(x)
+    assert np.array_equal(q.cpu().numpy(), wq)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), ws)
+    # odd widths use the streaming variant
+    x2 = randn_bf16((9, 8 * 64 * 17), 41)
+    q2, s2, _ = quant.scaled_int8_quant(to_dev(x2, dev))
+    wq2, ws2 = oq.token_quant(x2)
+    assert np.array_equal(q2.cpu().numpy(), wq2)
+    assert np.array_equal(s2.cpu().numpy().reshape(-1), ws2)
+
+
+def test_weight_quant_bit_exact(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import quant
+
+    w = randn_bf16((300, 1024), 50, std=0.02)
+    w[7] = 0.0
+    q, s = quant.quantize_weight(to_dev(w, dev))
+    torch.cuda.synchronize()
+    wq, wsc = oq.weight_quant(w)
+    assert np.array_equal(q.cpu().numpy(), wq)
+    assert np.array_equal(s.cpu().numpy().reshape(-1), wsc)
+
+
+@pytest.mark.parametrize("m,n,k", [(12, 32, 64), (300, 520, 1024), (513, 256, 5120)])
+def test_gemm_accumulators_and_epilogue_bit_exact(torch_mod, dev, m, n, k):
+    torch = torch_mod
+    from taomate_hd_amd import quant
+
+    rng = np.random.default_rng(m + n + k)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    a[0, :] = -128  # extreme accumulators
+    w[0, :] = -127
+    ad = torch.from_numpy(a).to(dev)
+    wd = torch.from_numpy(w).to(dev)
+    acc = quant.int8_mm_i32(ad, wd.t())
+    torch.cuda.synchronize()
+    want = oq.int_gemm(a, w)
+    assert np.array_equal(acc.cpu().numpy(), want)
+    sa = rng.random(m, dtype=np.float32) * 0.05 + 1e-3
+    sb = rng.random(n, dtype=np.float32) * 0.01 + 1e-4
+    bias = randn_bf16((n,), 60, std=0.02)
+    out = quant.cutlass_scaled_mm(
+        ad, wd.t(), torch.from_numpy(sa).to(dev).view(m, 1), torch.from_numpy(sb).to(dev).view(1, n),
+        torch.bfloat16, to_dev(bias, dev),
+    )
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(out), oq.scaled_mm_epilogue(want, sa, sb, bias))
+    out2 = quant.cutlass_scaled_mm(
+        ad, wd.t(), torch.from_numpy(sa).to(dev).view(m, 1), torch.from_numpy(sb).to(dev).view(1, n)
+    )
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(out2), oq.scaled_mm_epilogue(want, sa, sb, None))
