@@ -8,16 +8,20 @@
 // order and never concatenated.
 //
 // Work decomposition
-//   workgroup = 4 waves = 256 query rows of one head; each wave owns 64 rows
-//   (two 32-row MFMA column blocks) and keeps them, their fp32 output
-//   accumulators and the online-softmax state in registers (1 wave per SIMD).
-//   Keys stream through LDS in 64-token tiles, double-buffered: the next
-//   tile's global loads are in flight while the current tile is computed.
+//   workgroup = 4 waves = 128 query rows of one head; each wave owns 32 rows
+//   and keeps them, their fp32 output accumulators and the online-softmax
+//   state in registers (<= 256 VGPRs, two workgroups per CU, so two waves
+//   share each SIMD and the hardware overlaps one wave's softmax with the
+//   other's MFMAs).  Keys stream through LDS in 64-token tiles loaded with
+//   global_load_lds_dwordx4 (no VGRP staging), double-buffered: the next
+//   tile's loads are in flight while the current tile is computed.
 //   Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16
 //   (or v_mfma_i32_32x32x32_i8), so each lane holds 16 keys of one query
 //   column; the same registers, converted to bf16, are directly the B operand
 //   of O^T += V^T P^T.  The value slot layout (transposed, 4-token chunks
 //   interleaved) makes the matching A operand one 16-byte LDS read.
+//   LDS rows are XOR-swizzled per 16-byte chunk so that each 16-lane phase of
+//   a ds_read_b128 touches 16 distinct 16-byte bank groups.
 //   Online softmax works in log2 units with a lazy rescale: the running max
 //   is only moved (and O, l rescaled) when a tile exceeds it by 2^8.
 #include <math.h>
@@ -28,7 +32,7 @@ namespace tmhd {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kQW = 64;            // query rows per wave
+constexpr int kQW = 32;            // query rows per wave
 constexpr int kBM = kWaves * kQW;  // query rows per workgroup
 constexpr int kBN = 64;            // keys per tile
 constexpr float kLazyRescale = 8.0f;
@@ -80,6 +84,14 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// 16 bytes global -> LDS without a VGPR round trip.  `lds` is the wave's
+// 1 KiB destination block; lane i's bytes land at lds + 16 * i.
+__device__ __forceinline__ void load_lds16(const void *gptr, void *lds) {
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
+
 // Maps the linear workgroup id so that consecutive logical ids run on the same
 // XCD (the hardware deals workgroups round-robin over the 8 XCDs).  Logical
 // ids are head-major, so the workgroups that share one head's keys and values
@@ -90,203 +102,190 @@ __device__ __forceinline__ int xcd_logical_id(int b, int G) {
 }
 
 template <int D, bool I8>
-__global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_kernel(const KArgs a) {
   constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row
   constexpr int KCPR = KROW / 16;       // 16-byte chunks per key row
-  constexpr int KSW = (KCPR < 8 ? KCPR : 8) - 1;
+  constexpr int KRP = 256 / KROW;       // key rows per 256 bytes (one bank sweep)
   constexpr int KT = kBN * KROW;        // key tile bytes
   constexpr int VT = D * kBN * 2;       // value tile bytes (D rows of 64 keys)
-  constexpr int KLD = KT / (16 * 256);  // 16-byte loads per thread per tile
-  constexpr int VLD = VT / (16 * 256);
+  constexpr int KWL = KT / 1024 / kWaves;  // 1 KiB wave loads per wave per tile
+  constexpr int VWL = VT / 1024 / kWaves;
   constexpr int QST = I8 ? D / 32 : D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;
-  static_assert(KLD >= 1 && VLD >= 1, "tile too small for 256 threads");
+  static_assert(KWL >= 1 && VWL >= 1, "tile too small for 4 waves");
 
-  __shared__ __attribute__((aligned(16))) char smem[2 * (KT + VT)];
+  __shared__ __attribute__((aligned(1024))) char smem[2 * (KT + VT)];
+
+  // chunk swizzles: 16 consecutive rows (one 16-lane ds_read_b128 phase) hit
+  // 16 distinct 16-byte positions modulo 256 bytes
+  auto kswz = [](int row) { return (row / KRP) & (KCPR - 1); };
+  auto vswz = [](int row) { return (row >> 1) & 7; };
 
   const int L = xcd_logical_id(blockIdx.x, gridDim.x);
   const int h = L / a.nqt;
   const int qt = L - h * a.nqt;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
+  const int ql = qt * kBM + w * kQW + lr;  // this lane's query column
 
-  // ---- query operands (B operand of S^T = K Q^T), resident for the whole call
-  i32x4 qv[2][QST];
+  // ---- query operand (B operand of S^T = K Q^T), resident for the whole call
+  i32x4 qv[QST];
+  if (ql < a.lq) {
+    if constexpr (I8) {
+      const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int ql = qt * kBM + w * kQW + qb * 32 + lr;
-    if (ql < a.lq) {
-      if constexpr (I8) {
-        const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
-#pragma unroll
-        for (int st = 0; st < QST; ++st) qv[qb][st] = *(const i32x4 *)(p + st * 32);
-      } else {
-        const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
-        const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
-#pragma unroll
-        for (int st = 0; st < QST; ++st) qv[qb][st] = *(const i32x4 *)(p + st * 16);
-      }
+      for (int st = 0; st < QST; ++st) qv[st] = *(const i32x4 *)(p + st * 32);
     } else {
+      const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
+      const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
 #pragma unroll
-      for (int st = 0; st < QST; ++st) qv[qb][st] = i32x4{0, 0, 0, 0};
+      for (int st = 0; st < QST; ++st) qv[st] = *(const i32x4 *)(p + st * 16);
     }
+  } else {
+#pragma unroll
+    for (int st = 0; st < QST; ++st) qv[st] = i32x4{0, 0, 0, 0};
   }
   float qscale = 1.0f;
   if constexpr (I8) qscale = a.qs[(int64_t)h * a.qshs + (qt * kBM + w * kQW) / TMHD_QUANT_BLOCK];
 
-  f32x16 o[2][DB];
+  f32x16 o[DB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb)
+  for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[qb][db][r] = 0.0f;
-  float mref[2] = {-INFINITY, -INFINITY};
-  float lsum[2] = {0.0f, 0.0f};
+    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+  float mref = -INFINITY;
+  float lsum = 0.0f;
 
-  i32x4 kreg[KLD], vreg[VLD];
-  auto gload = [&](int s, int t) {
+  auto gload = [&](int s, int t, int buf) {
     const Seg &S = a.seg[s];
     const int t0 = t * kBN;
-    if constexpr (I8) {
-      const int8_t *kb = S.k8 + (int64_t)h * S.khs + (int64_t)t0 * D;
+    char *kd = smem + buf * (KT + VT);
+    char *vd = kd + KT;
+    const char *kg = I8 ? (const char *)(S.k8 + (int64_t)h * S.khs + (int64_t)t0 * D)
+                        : (const char *)(S.k + (int64_t)h * S.khs + (int64_t)t0 * D);
 #pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int c = i * 256 + tid, row = c / KCPR, ch = (c % KCPR) ^ (row & KSW);
-        kreg[i] = *(const i32x4 *)(kb + row * D + ch * 16);
-      }
-    } else {
-      const uint16_t *kb = S.k + (int64_t)h * S.khs + (int64_t)t0 * D;
-#pragma unroll
-      for (int i = 0; i < KLD; ++i) {
-        const int c = i * 256 + tid, row = c / KCPR, ch = (c % KCPR) ^ (row & KSW);
-        kreg[i] = *(const i32x4 *)(kb + row * D + ch * 8);
-      }
+    for (int i = 0; i < KWL; ++i) {
+      const int blk = w * KWL + i, c = blk * 64 + lane, row = c / KCPR;
+      load_lds16(kg + row * KROW + ((c % KCPR) ^ kswz(row)) * 16, kd + blk * 1024);
     }
-    const uint16_t *vb = S.vt + (int64_t)h * S.vhs + t0;
+    const char *vg = (const char *)(S.vt + (int64_t)h * S.vhs + t0);
 #pragma unroll
-    for (int i = 0; i < VLD; ++i) {
-      const int c = i * 256 + tid, row = c >> 3, ch = (c & 7) ^ (row & 7);
-      vreg[i] = *(const i32x4 *)(vb + (int64_t)row * S.vrs + ch * 8);
+    for (int i = 0; i < VWL; ++i) {
+      const int blk = w * VWL + i, c = blk * 64 + lane, row = c >> 3;
+      load_lds16(vg + (int64_t)row * S.vrs * 2 + ((c & 7) ^ vswz(row)) * 16, vd + blk * 1024);
     }
-  };
-  auto lstore = [&](int buf) {
-    char *kb = smem + buf * (KT + VT);
-    char *vb = kb + KT;
-#pragma unroll
-    for (int i = 0; i < KLD; ++i) *(i32x4 *)(kb + (i * 256 + tid) * 16) = kreg[i];
-#pragma unroll
-    for (int i = 0; i < VLD; ++i) *(i32x4 *)(vb + (i * 256 + tid) * 16) = vreg[i];
   };
 
   auto compute = [&](int buf, int s, int t) {
     const Seg &S = a.seg[s];
     const char *kb = smem + buf * (KT + VT);
     const char *vb = kb + KT;
-    const int nvalid = S.tokens - t * kBN;
+    const int nvalid = S.tokens - t * kBN;  // >= 1
+    const bool two = nvalid > 32;           // second 32-key block present
+    const bool partial = nvalid < kBN;
     float ct = a.c;
     if constexpr (I8) ct = a.c * qscale * S.ks[(int64_t)h * S.kshs + (t * kBN) / TMHD_QUANT_BLOCK];
+
+    // S^T for keys [32*kb, 32*kb+32): lane holds keys 32kb + 8(r/4) + 4g + r%4
+    f32x16 sc[2];
 #pragma unroll
     for (int kb32 = 0; kb32 < 2; ++kb32) {
-      if (kb32 * 32 >= nvalid) break;
+      if (kb32 == 1 && !two) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[1][r] = -INFINITY;
+        break;
+      }
       const int krow = kb32 * 32 + lr;
-      f32x16 sc[2];
+      i32x4 kk[QST];
+#pragma unroll
+      for (int st = 0; st < QST; ++st)
+        kk[st] = *(const i32x4 *)(kb + krow * KROW + ((2 * st + g) ^ kswz(krow)) * 16);
       if constexpr (I8) {
-        i32x16 ia[2];
+        i32x16 ia;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ia[0][r] = ia[1][r] = 0;
+        for (int r = 0; r < 16; ++r) ia[r] = 0;
 #pragma unroll
-        for (int st = 0; st < QST; ++st) {
-          const i32x4 kk = *(const i32x4 *)(kb + (krow * KCPR + ((2 * st + g) ^ (krow & KSW))) * 16);
-          ia[0] = mfma_i8(kk, qv[0][st], ia[0]);
-          ia[1] = mfma_i8(kk, qv[1][st], ia[1]);
-        }
+        for (int st = 0; st < QST; ++st) ia = mfma_i8(kk[st], qv[st], ia);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sc[0][r] = (float)ia[0][r];
-          sc[1][r] = (float)ia[1][r];
-        }
+        for (int r = 0; r < 16; ++r) sc[kb32][r] = (float)ia[r];
       } else {
+        f32x16 acc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sc[0][r] = sc[1][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
 #pragma unroll
-        for (int st = 0; st < QST; ++st) {
-          const i32x4 kk = *(const i32x4 *)(kb + (krow * KCPR + ((2 * st + g) ^ (krow & KSW))) * 16);
-          sc[0] = mfma_bf16(kk, qv[0][st], sc[0]);
-          sc[1] = mfma_bf16(kk, qv[1][st], sc[1]);
-        }
+        for (int st = 0; st < QST; ++st) acc = mfma_bf16(kk[st], qv[st], acc);
+        sc[kb32] = acc;
       }
-      // keys of this lane: kb32*32 + 8*(r/4) + 4*g + r%4
-      const int rem = nvalid - kb32 * 32;
-      const bool partial = rem < 32;
-      float cand[2];
+    }
+    // masked keys of a partial tile
+    if (partial) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        float m = -INFINITY;
+      for (int kb32 = 0; kb32 < 2; ++kb32)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const bool ok = !partial || (8 * (r >> 2) + 4 * g + (r & 3)) < rem;
-          m = ok ? fmaxf(m, sc[qb][r]) : m;
-        }
-        m = fmaxf(m, __shfl_xor(m, 32));
-        cand[qb] = m * ct;
-      }
-      const bool need = (cand[0] > mref[0] + kLazyRescale) || (cand[1] > mref[1] + kLazyRescale);
-      if (__any(need)) {
+        for (int r = 0; r < 16; ++r)
+          if (kb32 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) sc[kb32][r] = -INFINITY;
+    }
+    float m = sc[0][0];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          const float mn = fmaxf(mref[qb], cand[qb]);
-          const float alpha = (mref[qb] == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mref[qb] - mn);
-          lsum[qb] *= alpha;
+    for (int r = 1; r < 16; ++r) m = fmaxf(m, sc[0][r]);
 #pragma unroll
-          for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
-          mref[qb] = mn;
-        }
-      }
-      uint32_t pk[2][8];
+    for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[1][r]);
+    m = fmaxf(m, __shfl_xor(m, 32));
+    // masked logits stay -inf after scaling only if ct > 0; a zero INT8 block
+    // (ct == 0) must not turn -inf * 0 into NaN
+    const float cand = m == -INFINITY ? -INFINITY : m * ct;
+    if (__any(cand > mref + kLazyRescale)) {
+      const float mn = fmaxf(mref, cand);
+      const float alpha = (mref == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
+      lsum *= alpha;
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const float nm = -mref[qb];
+      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      mref = mn;
+    }
+    const float nm = -mref;
+    uint32_t pk[2][8];
+    const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-        for (int r = 0; r < 16; r += 2) {
-          float p0 = __builtin_amdgcn_exp2f(fmaf(sc[qb][r], ct, nm));
-          float p1 = __builtin_amdgcn_exp2f(fmaf(sc[qb][r + 1], ct, nm));
-          if (partial) {
-            p0 = (8 * (r >> 2) + 4 * g + (r & 3)) < rem ? p0 : 0.0f;
-            p1 = (8 * ((r + 1) >> 2) + 4 * g + ((r + 1) & 3)) < rem ? p1 : 0.0f;
+    for (int kb32 = 0; kb32 < 2; ++kb32) {
+      if (kb32 == 1 && !two) break;
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb32][r], ct, nm));
+        float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb32][r + 1], ct, nm));
+        if constexpr (I8) {
+          if (partial) {  // -inf * 0 guard for zero-scale blocks
+            p0 = sc[kb32][r] == -INFINITY ? 0.0f : p0;
+            p1 = sc[kb32][r + 1] == -INFINITY ? 0.0f : p1;
           }
-          pk[qb][r >> 1] = pack_bf16x2(p0, p1);
         }
-        float ls = lsum[qb];
-        const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-          ls = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[qb][i]), ones, ls, false);
-        lsum[qb] = ls;
+        pk[kb32][r >> 1] = pack_bf16x2(p0, p1);
       }
-      // O^T += V^T P^T over the 32 keys of this block (two 16-key steps)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const int vrow = db * 32 + lr;
+      for (int i = 0; i < 8; ++i)
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[kb32][i]), ones, lsum, false);
+    }
+    // O^T += V^T P^T, 16 keys per MFMA
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-          const i32x4 vv = *(const i32x4 *)(vb + (vrow * 8 + ((4 * kb32 + 2 * st + g) ^ (vrow & 7))) * 16);
+    for (int kb32 = 0; kb32 < 2; ++kb32) {
+      if (kb32 == 1 && !two) break;
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            const i32x4 pb = {(int)pk[qb][4 * st], (int)pk[qb][4 * st + 1], (int)pk[qb][4 * st + 2],
-                              (int)pk[qb][4 * st + 3]};
-            o[qb][db] = mfma_bf16(vv, pb, o[qb][db]);
-          }
+      for (int st = 0; st < 2; ++st) {
+        const i32x4 pb = {(int)pk[kb32][4 * st], (int)pk[kb32][4 * st + 1], (int)pk[kb32][4 * st + 2],
+                          (int)pk[kb32][4 * st + 3]};
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int vrow = db * 32 + lr;
+          const i32x4 vv = *(const i32x4 *)(vb + vrow * 128 + ((4 * kb32 + 2 * st + g) ^ vswz(vrow)) * 16);
+          o[db] = mfma_bf16(vv, pb, o[db]);
         }
       }
     }
   };
 
   // ---- key/value tile loop over the segment table
-  int s = 0, t = 0;
-  gload(s, t);
-  lstore(0);
+  int s = 0, t = 0, buf = 0;
+  gload(s, t, 0);
+  wait_vmem();
   __syncthreads();
-  int buf = 0;
   for (;;) {
     int ns = s, nt = t + 1;
     if (nt >= a.seg[s].ntiles) {
@@ -294,35 +293,30 @@ __global__ void __launch_bounds__(256, 1) attn_fwd_kernel(const KArgs a) {
       nt = 0;
     }
     const bool has_next = ns < a.nseg;
-    if (has_next) gload(ns, nt);
+    if (has_next) gload(ns, nt, buf ^ 1);
     compute(buf, s, t);
     if (!has_next) break;
-    lstore(buf ^ 1);
+    wait_vmem();
     __syncthreads();
     buf ^= 1;
     s = ns;
     t = nt;
   }
 
-  // ---- epilogue: O = O^T / l, written token-major
+  // ---- epilogue: O = O^T / l, written token-major (4 consecutive d per store)
+  const float lt = lsum + __shfl_xor(lsum, 32);
+  const float inv = 1.0f / lt;
+  if (ql < a.lq) {
+    const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
+    uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const float lt = lsum[qb] + __shfl_xor(lsum[qb], 32);
-    const float inv = 1.0f / lt;
-    const int ql = qt * kBM + w * kQW + qb * 32 + lr;
-    if (ql < a.lq) {
-      const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
-      uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const f32x16 &v = o[qb][db];
-          i32x2 pr = {(int)pack_bf16x2(v[4 * u] * inv, v[4 * u + 1] * inv),
-                      (int)pack_bf16x2(v[4 * u + 2] * inv, v[4 * u + 3] * inv)};
-          *(i32x2 *)(op + db * 32 + 8 * u) = pr;
-        }
-    }
+      for (int u = 0; u < 4; ++u) {
+        i32x2 pr = {(int)pack_bf16x2(o[db][4 * u] * inv, o[db][4 * u + 1] * inv),
+                    (int)pack_bf16x2(o[db][4 * u + 2] * inv, o[db][4 * u + 3] * inv)};
+        *(i32x2 *)(op + db * 32 + 8 * u) = pr;
+      }
   }
 }
 
