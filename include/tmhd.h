@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TMHD_MAX_SEGMENTS 8
+#define TMHD_MAX_SEGMENTS 16
 #define TMHD_KV_TILE 64
 #define TMHD_QUANT_BLOCK 128
 

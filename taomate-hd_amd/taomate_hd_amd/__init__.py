@@ -2,22 +2,94 @@
 
 A drop-in for the reference's per-layer streaming attention hook
 (src/taomate_hd/streaming/attention_hook.py), its clean audio-video KV cache
-(streaming/cache.py), the session around them (streaming/session.py) and the
-selective W8A8 projection ops (inference/w8a8.py).  All compute runs in the
-hand-written HIP kernels of libtmhd.so; nothing falls back to the CPU.
+(streaming/cache.py), the session around them (streaming/session.py,
+capability.py, policy.py) and the selective W8A8 projection ops
+(inference/w8a8.py, distributed/linear.py ``_linear``).  All compute runs in
+the hand-written HIP kernels of libtmhd.so; nothing falls back to the CPU.
 """
 
 from . import _native
 from .attention import QKQuantWorkspace, segment_attention
+from .capability import (
+    STREAM_HOOK_ABI,
+    native_stream_attention_hook,
+    native_stream_attention_metadata,
+    set_native_stream_attention_hook,
+    set_official_attention_hook,
+    streaming_capability,
+)
+from .hook import H3StreamingAttentionHook, HookMode, StreamingAttentionHook
+from .kvcache import (
+    AVKV,
+    AUDIO_TOKEN_TAG,
+    MAIN_LAYER_NAMES,
+    VIDEO_TOKEN_TAG,
+    CleanAVKVCache,
+    HeadMajorRingKVCache,
+    KVContract,
+    kv_contract_from_model,
+)
+from .quant import (
+    cutlass_scaled_mm,
+    cutlass_scaled_mm_out,
+    dynamic_scaled_int8_quant,
+    int8_mm_i32,
+    quantize_weight,
+    scaled_int8_quant,
+)
+from .session import H3StreamingSession, StreamingInferencePolicy, StreamingSession, apply_cross_chunk_cache_policy
 from .slots import KVSlot, SlotPool, SlotView, vt_position
+from .w8a8 import (
+    CutlassW8A8Workspace,
+    W8A8Workspace,
+    cutlass_w8a8_linear,
+    linear,
+    quantize_cutlass_w8a8_weight,
+    register_torch_ops,
+    resolve_h3_cutlass_w8a8_policy,
+)
 
 __all__ = [
     "_native",
-    "QKQuantWorkspace",
-    "segment_attention",
+    "AVKV",
+    "AUDIO_TOKEN_TAG",
+    "CleanAVKVCache",
+    "CutlassW8A8Workspace",
+    "H3StreamingAttentionHook",
+    "H3StreamingSession",
+    "HeadMajorRingKVCache",
+    "HookMode",
+    "KVContract",
     "KVSlot",
+    "MAIN_LAYER_NAMES",
+    "QKQuantWorkspace",
+    "STREAM_HOOK_ABI",
     "SlotPool",
     "SlotView",
+    "StreamingAttentionHook",
+    "StreamingInferencePolicy",
+    "StreamingSession",
+    "VIDEO_TOKEN_TAG",
+    "W8A8Workspace",
+    "apply_cross_chunk_cache_policy",
+    "cutlass_scaled_mm",
+    "cutlass_scaled_mm_out",
+    "cutlass_w8a8_linear",
+    "dynamic_scaled_int8_quant",
+    "int8_mm_i32",
+    "kv_contract_from_model",
+    "linear",
+    "native_stream_attention_hook",
+    "native_stream_attention_metadata",
+    "quantize_cutlass_w8a8_weight",
+    "quantize_weight",
+    "register_torch_ops",
+    "resolve_h3_cutlass_w8a8_policy",
+    "scaled_int8_quant",
+    "segment_attention",
+    "set_native_stream_attention_hook",
+    "set_official_attention_hook",
+    "streaming_capability",
     "vt_position",
 ]
 

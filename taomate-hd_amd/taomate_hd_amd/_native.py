@@ -13,7 +13,7 @@ from pathlib import Path
 from typing import Any
 
 LIB_PATH = Path(__file__).with_name("libtmhd.so")
-MAX_SEGMENTS = 8
+MAX_SEGMENTS = 16
 KV_TILE = 64
 QUANT_BLOCK = 128
 QUERY_TILE = 256

@@ -1,0 +1,176 @@
+"""Selective W8A8 projection: drop-in for src/taomate_hd/inference/w8a8.py and
+the ``_linear`` dispatch of src/taomate_hd/distributed/linear.py:43-68.
+
+* ``W8A8Workspace`` mirrors ``CutlassW8A8Workspace`` (w8a8.py:12-73): grow-only
+  activation / scale / output buffers per (device, stream, width), then
+  ``dynamic_scaled_int8_quant`` + ``cutlass_scaled_mm`` into them.
+* ``cutlass_w8a8_linear`` (w8a8.py:117-145) also accepts a bf16 bias, applied
+  in the GEMM epilogue (the reference raises for a bias).
+* ``resolve_h3_cutlass_w8a8_policy`` restates the interior QKV/FC1 selection
+  (w8a8.py:89-114); ``quantize_cutlass_w8a8_weight`` the weight quantizer
+  (w8a8.py:175-179, run as a HIP kernel).
+* ``linear`` is the ``_linear`` dispatch rule: a module that carries a W8A8
+  weight scale takes the INT8 path, otherwise ``F.linear``.
+* ``register_torch_ops`` exposes the two ops as ``torch.ops.tmhd.*`` with the
+  ``torch.ops._C`` signatures the reference's workspace resolves by name.
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+from . import quant
+
+INTERIOR_FC1_QKV_CUTLASS_W8A8_POLICY = "interior_fc1_qkv_v1"
+H3_CUTLASS_W8A8_POLICIES = (INTERIOR_FC1_QKV_CUTLASS_W8A8_POLICY,)
+
+
+class W8A8Workspace:
+    """Reusable per-stream INT8 activation and bf16 output storage (w8a8.py:12-73)."""
+
+    def __init__(self, torch: Any) -> None:
+        self._torch = torch
+        self._activation: dict[tuple[Any, ...], tuple[Any, Any]] = {}
+        self._outputs: dict[tuple[Any, ...], Any] = {}
+
+    def _stream_key(self, inputs: Any) -> tuple[Any, ...]:
+        device = inputs.device
+        if device.type != "cuda":
+            return (device.type, device.index, 0)
+        stream = self._torch.cuda.current_stream(device=device)
+        return (device.type, device.index, int(stream.cuda_stream))
+
+    def _activation_buffers(self, inputs: Any, stream_key: tuple[Any, ...]) -> tuple[Any, Any]:
+        rows, width = int(inputs.shape[0]), int(inputs.shape[1])
+        key = (*stream_key, width)
+        existing = self._activation.get(key)
+        if existing is None or int(existing[0].shape[0]) < rows:
+            existing = (
+                self._torch.empty((rows, width), device=inputs.device, dtype=self._torch.int8),
+                self._torch.empty((rows, 1), device=inputs.device, dtype=self._torch.float32),
+            )
+            self._activation[key] = existing
+        return existing[0][:rows], existing[1][:rows]
+
+    def _output_buffer(self, inputs: Any, output_width: int, stream_key: tuple[Any, ...]) -> Any:
+        rows = int(inputs.shape[0])
+        key = (*stream_key, int(output_width))
+        existing = self._outputs.get(key)
+        if existing is None or int(existing.shape[0]) < rows:
+            existing = self._torch.empty((rows, int(output_width)), device=inputs.device, dtype=self._torch.bfloat16)
+            self._outputs[key] = existing
+        return existing[:rows]
+
+    def linear(self, inputs: Any, weight_t: Any, weight_scale: Any, bias: Any | None = None) -> Any:
+        stream_key = self._stream_key(inputs)
+        quantized, activation_scale = self._activation_buffers(inputs, stream_key)
+        output = self._output_buffer(inputs, int(weight_t.shape[1]), stream_key)
+        quant.dynamic_scaled_int8_quant(quantized, inputs, activation_scale, None)
+        quant.cutlass_scaled_mm_out(output, quantized, weight_t, activation_scale, weight_scale, bias)
+        return output
+
+
+# the reference's class name
+CutlassW8A8Workspace = W8A8Workspace
+
+
+def resolve_h3_cutlass_w8a8_policy(linear_names: list[str], *, policy: str) -> dict[str, Any]:
+    """Select the interior QKV/FC1 projections for W8A8 (w8a8.py:89-114)."""
+    if policy not in H3_CUTLASS_W8A8_POLICIES:
+        raise ValueError("unsupported H3 CUTLASS W8A8 policy")
+    projection_names = [name for name in linear_names if name.endswith((".attn.qkv_proj", ".mlp.fc1", ".mlp.fc2"))]
+    if not projection_names:
+        raise ValueError("H3 CUTLASS W8A8 policy requires projection candidates")
+    block_indices = sorted({int(name.split(".", 2)[1]) for name in projection_names})
+    boundary_blocks = (*block_indices[:2], *block_indices[-3:])
+    eligible_suffixes = (".attn.qkv_proj", ".mlp.fc1")
+    quantized_names = [
+        name
+        for name in projection_names
+        if name.endswith(eligible_suffixes) and int(name.split(".", 2)[1]) not in boundary_blocks
+    ]
+    quantized_set = set(quantized_names)
+    return {
+        "policy": policy,
+        "quantized_linear_names": quantized_names,
+        "bf16_protected_linear_names": [name for name in projection_names if name not in quantized_set],
+        "bf16_boundary_block_indices": list(boundary_blocks),
+    }
+
+
+def quantize_cutlass_w8a8_weight(torch: Any, weight: Any) -> tuple[Any, Any]:
+    """Exact W8 conversion (w8a8.py:175-179): returns (q [N, K] int8, scale [N, 1] fp32)."""
+    del torch
+    return quant.quantize_weight(weight)
+
+
+def cutlass_w8a8_linear(
+    torch: Any,
+    inputs: Any,
+    weight: Any,
+    weight_scale: Any,
+    *,
+    bias: Any | None,
+    workspace: W8A8Workspace | None = None,
+    weight_t: Any | None = None,
+    weight_scale_t: Any | None = None,
+) -> Any:
+    """Dynamic per-token A8 x per-channel W8 GEMM (w8a8.py:117-145), bf16 out."""
+    shape = (*inputs.shape[:-1], int(weight.shape[0]))
+    flattened = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
+    w_t = weight.t() if weight_t is None else weight_t
+    s_t = weight_scale.t() if weight_scale_t is None else weight_scale_t
+    if workspace is not None:
+        return workspace.linear(flattened, w_t, s_t, bias).reshape(shape)
+    quantized, activation_scale, _ = quant.scaled_int8_quant(flattened)
+    output = quant.cutlass_scaled_mm(quantized, w_t, activation_scale, s_t, torch.bfloat16, bias)
+    return output.reshape(shape)
+
+
+def linear(
+    torch: Any,
+    inputs: Any,
+    weight: Any,
+    bias: Any | None,
+    *,
+    cutlass_w8a8_weight_scale: Any | None = None,
+    cutlass_w8a8_workspace: W8A8Workspace | None = None,
+    cutlass_w8a8_weight_t: Any | None = None,
+    cutlass_w8a8_weight_scale_t: Any | None = None,
+) -> Any:
+    """The ``_linear`` dispatch (distributed/linear.py:43-68) without its dead FP8 branch."""
+    if cutlass_w8a8_weight_scale is not None:
+        return cutlass_w8a8_linear(
+            torch,
+            inputs,
+            weight,
+            cutlass_w8a8_weight_scale,
+            bias=bias,
+            workspace=cutlass_w8a8_workspace,
+            weight_t=cutlass_w8a8_weight_t,
+            weight_scale_t=cutlass_w8a8_weight_scale_t,
+        )
+    return torch.nn.functional.linear(inputs, weight, bias)
+
+
+_REGISTERED = False
+
+
+def register_torch_ops() -> Any:
+    """Register ``torch.ops.tmhd.dynamic_scaled_int8_quant`` and
+    ``torch.ops.tmhd.cutlass_scaled_mm`` (out-variants with the argument order
+    of ``torch.ops._C`` used at w8a8.py:71-72); returns ``torch.ops.tmhd``."""
+    global _REGISTERED
+    import torch
+
+    if not _REGISTERED:
+        lib = torch.library.Library("tmhd", "DEF")
+        lib.define("dynamic_scaled_int8_quant(Tensor(a!) out, Tensor x, Tensor(b!) scale, Tensor? azp) -> ()")
+        lib.define(
+            "cutlass_scaled_mm(Tensor(a!) out, Tensor a, Tensor b, Tensor a_scales, Tensor b_scales, Tensor? bias) -> ()"
+        )
+        lib.impl("dynamic_scaled_int8_quant", quant.dynamic_scaled_int8_quant, "CUDA")
+        lib.impl("cutlass_scaled_mm", quant.cutlass_scaled_mm_out, "CUDA")
+        register_torch_ops._lib = lib  # keep the registration alive
+        _REGISTERED = True
+    return torch.ops.tmhd

@@ -1,0 +1,243 @@
+"""The streaming hook + in-place KV cache on the GPU against the oracle's CPU
+restatement of the reference hook and cache, over whole streaming sequences."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle import bf16
+from oracle import stream as ost
+from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAX_ABS = 2e-2
+BF16_MEAN_ABS = 1e-3
+I8_COSINE = 0.999
+LAYERS = ("blocks.0.attn", "blocks.1.attn")
+H, D = 2, 128
+
+
+class _Attn:
+    softmax_scale = D ** -0.5
+
+
+def _check(backend, got, want, exact=None):
+    if backend == "sdpa":
+        mx, mean = err_stats(got, want)
+        assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+    else:
+        ref = want if exact is None else exact
+        assert oatt.cosine(got, ref) >= I8_COSINE
+
+
+def _qkv(t, seed):
+    q = randn_bf16((t, H, D), seed)
+    k = randn_bf16((t, H, D), seed + 1, offset=key_offset(H, D, seed + 2))
+    v = randn_bf16((t, H, D), seed + 3)
+    return q, k, v
+
+
+def _call(torch, dev, hook, oracle_hook, layer, q, k, v, tags, mask, bounds, hint=None):
+    out = hook(
+        attention=_Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev), value=to_dev(v, dev),
+        token_tags=torch.tensor(tags, device=dev), commit_mask=torch.tensor(mask, device=dev),
+        cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=tuple(bounds),
+        max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])), live_documents_hint=hint,
+    )
+    torch.cuda.synchronize()
+    want = oracle_hook(layer, q, k, v, tags, mask, bounds, D ** -0.5, live_documents_hint=hint)
+    return bf16.from_torch(out), want
+
+
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_stream_noisy_commit_retain_sequence(torch_mod, dev, backend):
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd.hook import HookMode
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
+    ocache = ost.CacheOracle(LAYERS)
+    ohook = ost.HookOracle(ocache, backend=backend)
+    exact_cache = ost.CacheOracle(LAYERS)
+    exact_hook = ost.HookOracle(exact_cache, backend="sdpa")
+    # packed layout [text 37, cond 20, audio 14, video 90, pad] -> 161 used, 192 rows
+    tags, mask, bounds = ost.packed_layout(37, 20, 14, 90)
+    T = len(tags)
+    seed = 100
+    for block in range(5):
+        for mode in ("noisy", "clean_commit"):
+            if mode == "clean_commit":
+                cache.begin_clean_commit(block)
+                ocache.begin_clean_commit(block)
+                exact_cache.begin_clean_commit(block)
+            hook.activate(mode=HookMode(mode), block_index=block)
+            ohook.activate(mode, block)
+            exact_hook.activate(mode, block)
+            for layer in LAYERS:
+                q, k, v = _qkv(T, seed)
+                seed += 10
+                got, want = _call(torch, dev, hook, ohook, layer, q, k, v, tags, mask, bounds)
+                exact = exact_hook(layer, q, k, v, tags, mask, bounds, D ** -0.5)
+                _check(backend, got, want, exact)
+            hook.deactivate()
+            ohook.deactivate()
+            exact_hook.deactivate()
+            if mode == "clean_commit":
+                cache.commit()
+                ocache.commit()
+                exact_cache.commit()
+                cache.retain_sink_and_recent_commits(2)
+                ocache.retain_sink_and_recent_commits(2)
+                exact_cache.retain_sink_and_recent_commits(2)
+        # ledger and stored history are identical to the reference semantics
+        assert cache.committed_blocks == ocache.block_index
+        assert list(cache.commit_token_counts) == ocache.counts
+        assert list(cache.commit_token_tags) == ocache.tags
+        for layer in LAYERS:
+            pair = cache.history(layer)
+            want_k, want_v = ocache.history(layer)
+            assert np.array_equal(bf16.from_torch(pair.key), want_k)
+            assert np.array_equal(bf16.from_torch(pair.value), want_v)
+    assert cache.retained_blocks == 3  # sink + 2 recent
+    assert cache.history_video_tokens == ocache.counts[0] + 2 * 90
+    if backend == "sage_attn":
+        receipt = hook.attention_backend_receipt()
+        assert receipt["kernel_calls"] > 0 and receipt["smooth_k"]
+
+
+def test_stream_fused_progress_denoise(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd.hook import HookMode
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
+    hook = StreamingAttentionHook(cache)
+    ocache = ost.CacheOracle(LAYERS)
+    ohook = ost.HookOracle(ocache)
+    tags1, mask1, b1 = ost.packed_layout(9, 0, 6, 40, align=8)
+    tags2, mask2, b2 = ost.packed_layout(5, 0, 8, 48, align=8)
+    # packed pair: previous document (being committed) + current document
+    tags = np.concatenate([tags1, tags2])
+    mask = np.concatenate([mask1, mask2])
+    bounds = (*b1, *(len(tags1) + b for b in b2[1:]))
+    seed = 500
+
+    def run(mode, block, layout, hint=None, **kw):
+        nonlocal seed
+        t_, m_, b_ = layout
+        hook.activate(mode=HookMode(mode), block_index=block, **kw)
+        ohook.activate(mode, block, kw.get("fused_current_use_sink"), kw.get("fused_current_recent_blocks"))
+        for layer in LAYERS:
+            q, k, v = _qkv(len(t_), seed)
+            seed += 10
+            got, want = _call(torch, dev, hook, ohook, layer, q, k, v, t_, m_, b_, hint=hint)
+            _check("sdpa", got, want)
+        hook.deactivate()
+        ohook.deactivate()
+
+    for block in range(4):
+        # fused variants against the current cache depth (rolled back)
+        for recent, sink in ((2, True), (3, True), (1, True), (2, False), (None, None)):
+            kw = {} if recent is None else {"fused_current_use_sink": sink, "fused_current_recent_blocks": recent}
+            cache.begin_clean_commit(block)
+            ocache.begin_clean_commit(block)
+            run("fused_progress_denoise", block, (tags, mask, bounds), hint=(0, 2), **kw)
+            cache.rollback()
+            ocache.rollback()
+        # then commit this block through a fused step (or a plain clean commit)
+        cache.begin_clean_commit(block)
+        ocache.begin_clean_commit(block)
+        if block % 2:
+            run("fused_progress_denoise", block, (tags, mask, bounds), fused_current_use_sink=True,
+                fused_current_recent_blocks=2)
+        else:
+            run("clean_commit", block, (tags1, mask1, b1))
+        cache.commit()
+        ocache.commit()
+        cache.retain_sink_and_recent_commits(2)
+        ocache.retain_sink_and_recent_commits(2)
+        assert list(cache.commit_token_tags) == ocache.tags
+        for layer in LAYERS:
+            pair = cache.history(layer)
+            wk, wv = ocache.history(layer)
+            assert np.array_equal(bf16.from_torch(pair.key), wk)
+            assert np.array_equal(bf16.from_torch(pair.value), wv)
+            if block >= 1:
+                fk = cache.history_for_fused_current(layer, use_sink=True, recent_blocks=2)
+                ok, ov = ocache.history_for_fused_current(layer, use_sink=True, recent_blocks=2)
+                assert np.array_equal(bf16.from_torch(fk.key), ok)
+                assert np.array_equal(bf16.from_torch(fk.value), ov)
+
+
+def test_noncontiguous_commit_mask_and_empty_documents(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd.hook import HookMode
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS[:1], local_heads=H, head_dim=D))
+    hook = StreamingAttentionHook(cache)
+    ocache = ost.CacheOracle(LAYERS[:1])
+    ohook = ost.HookOracle(ocache)
+    T = 150
+    rng = np.random.default_rng(3)
+    mask = np.zeros(T, dtype=bool)
+    mask[10:140] = rng.random(130) < 0.7  # interleaved condition/media rows
+    tags = np.where(rng.random(T) < 0.5, 0, 2).astype(np.int64)
+    tags[~mask] = 1
+    tags[mask & (np.arange(T) % 7 == 0)] = 2
+    tags[mask & (np.arange(T) % 7 == 1)] = 0
+    bounds = (0, 0, 140, 140, 150)  # empty documents at both ends of the live one
+    for block, mode in ((0, "noisy"), (0, "clean_commit"), (1, "noisy")):
+        if mode == "clean_commit":
+            cache.begin_clean_commit(block)
+            ocache.begin_clean_commit(block)
+        hook.activate(mode=HookMode(mode), block_index=block)
+        ohook.activate(mode, block)
+        q, k, v = _qkv(T, 900 + block)
+        got, want = _call(torch, dev, hook, ohook, LAYERS[0], q, k, v, tags, mask, bounds)
+        _check("sdpa", got, want)
+        hook.deactivate()
+        ohook.deactivate()
+        if mode == "clean_commit":
+            cache.commit()
+            ocache.commit()
+    pair = cache.history(LAYERS[0])
+    wk, wv = ocache.history(LAYERS[0])
+    assert np.array_equal(bf16.from_torch(pair.key), wk)
+    assert np.array_equal(bf16.from_torch(pair.value), wv)
+
+
+def test_session_rollback_on_error(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingSession
+
+    class Plan:
+        phases = ("p0", "p1", "p2")
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
+    tags, mask, bounds = ost.packed_layout(4, 0, 4, 24, align=8)
+    T = len(tags)
+    with StreamingSession(Plan(), cache=cache) as session:
+        with session.noisy_step(0):
+            pass
+        with pytest.raises(RuntimeError, match="boom"):
+            with session.clean_commit(0):
+                q, k, v = (to_dev(x, dev) for x in _qkv(T, 5))
+                session.hook(attention=_Attn(), layer_name=LAYERS[0], query=q, key=k, value=v,
+                             token_tags=torch.tensor(tags, device=dev), commit_mask=torch.tensor(mask, device=dev),
+                             cu_seqlens=None, cu_seqlens_host=bounds, max_seqlen=T)
+                assert cache.clean_commit_active
+                raise RuntimeError("boom")
+        assert not cache.clean_commit_active and cache.committed_blocks == 0 and cache.retained_blocks == 0
+        # a commit missing a layer is rejected and rolled back
+        with pytest.raises(RuntimeError, match="missing attention layers"):
+            with session.clean_commit(0):
+                q, k, v = (to_dev(x, dev) for x in _qkv(T, 6))
+                session.hook(attention=_Attn(), layer_name=LAYERS[0], query=q, key=k, value=v,
+                             token_tags=torch.tensor(tags, device=dev), commit_mask=torch.tensor(mask, device=dev),
+                             cu_seqlens=None, cu_seqlens_host=bounds, max_seqlen=T)
+        assert cache.committed_blocks == 0 and not cache.clean_commit_active

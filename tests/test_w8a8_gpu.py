@@ -1,0 +1,69 @@
+"""The W8A8 projection module (workspace, dispatch, torch ops) on the GPU."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import bf16
+from oracle import quant as oq
+from tests.helpers import randn_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+def _expected(x, w, bias=None):
+    qx, sx = oq.token_quant(x)
+    qw, sw = oq.weight_quant(w)
+    acc = oq.int_gemm(qx, qw)
+    return oq.scaled_mm_epilogue(acc, sx, sw, bias)
+
+
+def test_cutlass_w8a8_linear_paths_bit_exact(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import W8A8Workspace, cutlass_w8a8_linear, linear, quantize_cutlass_w8a8_weight
+
+    x = randn_bf16((3, 50, 512), 70)  # [..., K] activations, flattened to 150 rows
+    x[..., 11] *= 20.0
+    x = bf16.round_f32(x)
+    w = randn_bf16((384, 512), 71, std=0.02)
+    bias = randn_bf16((384,), 72, std=0.02)
+    qw, sw = quantize_cutlass_w8a8_weight(torch, to_dev(w, dev))
+    want = _expected(x.reshape(-1, 512), w).reshape(3, 50, 384)
+    xd = to_dev(x, dev)
+    out = cutlass_w8a8_linear(torch, xd, qw, sw, bias=None)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(out), want)
+    ws = W8A8Workspace(torch)
+    for rows in (150, 40, 150):  # grow, shrink (reuse), reuse
+        xr = xd.reshape(-1, 512)[:rows]
+        o2 = cutlass_w8a8_linear(torch, xr, qw, sw, bias=to_dev(bias, dev), workspace=ws)
+        torch.cuda.synchronize()
+        assert np.array_equal(bf16.from_torch(o2), _expected(x.reshape(-1, 512)[:rows], w, bias))
+    # dispatch rule of _linear: with a scale -> W8A8, without -> F.linear
+    o3 = linear(torch, xd, qw, None, cutlass_w8a8_weight_scale=sw)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(o3), want)
+    wd = to_dev(w, dev)
+    o4 = linear(torch, xd, wd, None)
+    assert o4.dtype == torch.bfloat16 and tuple(o4.shape) == (3, 50, 384)
+
+
+def test_registered_torch_ops(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import register_torch_ops
+
+    ops = register_torch_ops()
+    x = randn_bf16((64, 256), 80)
+    w = randn_bf16((128, 256), 81, std=0.02)
+    xd = to_dev(x, dev)
+    q = torch.empty((64, 256), dtype=torch.int8, device=dev)
+    s = torch.empty((64, 1), dtype=torch.float32, device=dev)
+    ops.dynamic_scaled_int8_quant(q, xd, s, None)
+    from taomate_hd_amd import quantize_weight
+
+    qw, sw = quantize_weight(to_dev(w, dev))
+    out = torch.empty((64, 128), dtype=torch.bfloat16, device=dev)
+    ops.cutlass_scaled_mm(out, q, qw.t(), s, sw.t(), None)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(out), _expected(x, w))
