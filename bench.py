@@ -1,0 +1,348 @@
+#!/usr/bin/env python3
+"""Benchmark of the TaoMate-HD streaming attention hot path on one MI355X.
+
+A step is one layer-call of the streaming attention hook at the 768p stage
+(BF16 backend): the current chunk's 12,252 queries attend over the cached
+video anchor (4,032 tokens) and two 12,252-token history chunks, read in
+place from the cache's slots, plus the chunk's own 12,252 keys/values, which
+the hook packs into a slot first.  H = 40, D = 128, no mask; Q/K/V ~ N(0, 1)
+bf16 with a per-(head, channel) key offset ~ N(0, 0.5), synthetic data.
+The same step with the INT8-QK backend and the W8A8 projection
+(12,252 x 5,120 -> 13,824, per-token INT8 X, per-channel INT8 W, bf16 bias)
+are measured beside it and reported in the same JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|bf16|i8qk|w8a8] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for _p in (str(REPO), str(REPO / "taomate-hd_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "attention TFLOPS & µs/layer-call (BF16, INT8-QK) at 768p stage; % MFMA peak"
+# MI355X dense peaks: 256 CUs x 2.4 GHz x (4,096 bf16 flop | 8,192 int8 op) per CU-clock; HBM3E 8 TB/s
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_INT8_TOPS = 5033.2
+PEAK_HBM_GBPS = 8000.0
+
+H, D = 40, 128
+LQ = 12252  # 3 latent frames x 48 x 84 video tokens + 156 audio tokens
+VIDEO, AUDIO = 12096, 156
+ANCHOR = 4032
+LKV = LQ + ANCHOR + 2 * LQ  # 40,788
+ATTN_FLOPS = 4.0 * H * LQ * LKV * D
+LAYER = "blocks.0.attn"
+M_X, K_X, N_W = 12252, 5120, 13824
+TRAFFIC_PROFILE = REPO / "profiles" / "attn_fwd_bf16_768p_pmc.txt"
+
+
+def _log(msg: str) -> None:
+    sys.stderr.write(msg + "\n")
+    sys.stderr.flush()
+
+
+class _Attn:
+    softmax_scale = D ** -0.5
+
+
+def _randn(torch, shape, gen, dev, std=1.0):
+    return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std
+
+
+def build_stream(torch, dev, timer):
+    """A cache holding the 768p anchor + two history chunks, and one chunk's inputs."""
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    offset = _randn(torch, (H, D), gen, dev, 0.5)
+    contract = KVContract(layer_names=(LAYER,), local_heads=H, head_dim=D)
+    cache = HeadMajorRingKVCache(contract)
+
+    def chunk(n_video, n_audio):
+        n = n_video + n_audio
+        q = _randn(torch, (n, H, D), gen, dev).to(torch.bfloat16)
+        k = (_randn(torch, (n, H, D), gen, dev) + offset).to(torch.bfloat16)
+        v = _randn(torch, (n, H, D), gen, dev).to(torch.bfloat16)
+        tags = torch.cat(
+            [torch.full((n_audio,), 2, dtype=torch.long, device=dev), torch.zeros(n_video, dtype=torch.long, device=dev)]
+        )
+        return q, k, v, tags, torch.ones(n, dtype=torch.bool, device=dev)
+
+    # block 0 becomes the video-only anchor once two newer blocks exist
+    for block, (nv, na) in enumerate([(ANCHOR, AUDIO), (VIDEO, AUDIO), (VIDEO, AUDIO)]):
+        _, k, v, tags, mask = chunk(nv, na)
+        cache.begin_clean_commit(block)
+        cache.stage(LAYER, k, v, tags, mask)
+        cache.commit()
+        cache.retain_sink_and_recent_commits(2)
+    assert cache.history_tokens == ANCHOR + 2 * LQ, cache.history_tokens
+    q, k, v, tags, mask = chunk(VIDEO, AUDIO)
+    inputs = dict(query=q, key=k, value=v, token_tags=tags, commit_mask=mask)
+    return cache, inputs
+
+
+def hook_step(hook, inputs, cu):
+    return hook(
+        attention=_Attn(), layer_name=LAYER, cu_seqlens=cu, cu_seqlens_host=(0, LQ), max_seqlen=LQ, **inputs
+    )
+
+
+def time_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    return wall_ms, start.elapsed_time(end) / steps
+
+
+def bench_attention(torch, dev, backend, steps, warmup, cache, inputs):
+    from taomate_hd_amd import HookMode, StreamingAttentionHook
+    from taomate_hd_amd.profiling import ComponentTimer
+
+    timer = ComponentTimer(torch)
+    hook = StreamingAttentionHook(cache, attention_backend=backend, timer=timer)
+    hook.activate(mode=HookMode.NOISY, block_index=cache.committed_blocks)
+    cu = torch.tensor([0, LQ], dtype=torch.int32, device=dev)
+    out = None
+
+    def step():
+        nonlocal out
+        out = hook_step(hook, inputs, cu)
+
+    for _ in range(warmup):
+        step()
+    timer.reset()
+    wall_ms, dev_ms = time_steps(torch, step, steps, 0)
+    comps = timer.summary()
+    hook.deactivate()
+    if not bool(torch.isfinite(out).all()):
+        raise RuntimeError(f"{backend} attention produced non-finite output")
+    return wall_ms, dev_ms, comps
+
+
+def bench_w8a8(torch, dev, steps, warmup):
+    from taomate_hd_amd import W8A8Workspace, cutlass_w8a8_linear, quant
+    from taomate_hd_amd.profiling import ComponentTimer
+
+    gen = torch.Generator(device=dev).manual_seed(4)
+    x = _randn(torch, (M_X, K_X), gen, dev)
+    gsel = torch.Generator(device="cpu").manual_seed(6)
+    outliers = torch.randperm(K_X, generator=gsel)[: K_X // 100].to(dev)
+    x[:, outliers] *= 20.0
+    x = x.to(torch.bfloat16)
+    w = _randn(torch, (N_W, K_X), torch.Generator(device=dev).manual_seed(5), dev, 0.02).to(torch.bfloat16)
+    bias = _randn(torch, (N_W,), gen, dev, 0.02).to(torch.bfloat16)
+    qw, sw = quant.quantize_weight(w)  # load-time, not timed
+    qw_t, sw_t = qw.t(), sw.t()
+    ws = W8A8Workspace(torch)
+    wall_ms, dev_ms = time_steps(
+        torch, lambda: cutlass_w8a8_linear(torch, x, qw, sw, bias=bias, workspace=ws, weight_t=qw_t, weight_scale_t=sw_t),
+        steps, warmup,
+    )
+    timer = ComponentTimer(torch)
+    q = torch.empty((M_X, K_X), dtype=torch.int8, device=dev)
+    s = torch.empty((M_X, 1), dtype=torch.float32, device=dev)
+    out = torch.empty((M_X, N_W), dtype=torch.bfloat16, device=dev)
+    for i in range(steps + warmup):
+        if i == warmup:
+            timer.reset()
+        with timer.region("token_quant"):
+            quant.dynamic_scaled_int8_quant(q, x, s)
+        with timer.region("gemm"):
+            quant.cutlass_scaled_mm_out(out, q, qw_t, s, sw_t, bias)
+    comps = timer.summary()
+    return wall_ms, dev_ms, comps
+
+
+def cpu_baseline(torch):
+    """The reference serial backend (torch SDPA, fp32) on the host cores, 768p shapes, a head subset."""
+    from oracle.attention import sdpa_cpu
+
+    threads = torch.get_num_threads()
+    gen = torch.Generator().manual_seed(0)
+    heads_used, times = 0, []
+    for heads in (1, 2):
+        q = torch.randn(LQ, heads, D, generator=gen).to(torch.bfloat16).float()
+        k = torch.randn(LKV, heads, D, generator=gen).to(torch.bfloat16).float()
+        v = torch.randn(LKV, heads, D, generator=gen).to(torch.bfloat16).float()
+        t0 = time.perf_counter()
+        sdpa_cpu(q, k, v, D ** -0.5)
+        first = time.perf_counter() - t0
+        runs = [first]
+        while sum(runs) < 6.0 and len(runs) < 3:
+            t0 = time.perf_counter()
+            sdpa_cpu(q, k, v, D ** -0.5)
+            runs.append(time.perf_counter() - t0)
+        heads_used, times = heads, runs
+        if sum(runs) > 8.0:
+            break
+    t = statistics.median(times)
+    flops = 4.0 * heads_used * LQ * LKV * D
+    return {
+        "value": round(flops / t / 1e12, 4),
+        "unit": "TFLOPS",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"torch SDPA fp32 on CPU (reference serial backend), 768p shapes Lq {LQ} x Lkv {LKV}, "
+            f"{heads_used} of {H} heads, median of {len(times)} runs ({t:.2f} s each); "
+            f"whole-call equivalent x{H // heads_used} = {t * H / heads_used * 1e3:.0f} ms"
+        ),
+    }
+
+
+def read_traffic():
+    """HBM bytes per attention launch from the committed rocprof counter summary, if any."""
+    if not TRAFFIC_PROFILE.exists():
+        return None
+    for line in TRAFFIC_PROFILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8"), default="all")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        _log(
+            f"bench.py runs on one GPU only (--gpus {args.gpus}, WORLD_SIZE {world}): the streaming attention "
+            "hot path is measured on a single MI355X; multi-GPU sharding is by heads and not run here."
+        )
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        _log("bench.py needs a GPU")
+        return 1
+    from taomate_hd_amd import _native
+
+    _native.load()
+    dev = torch.device("cuda:0")
+    props = torch.cuda.get_device_properties(dev)
+    _log(f"device {props.name} {getattr(props, 'gcnArchName', '')} CUs {props.multi_processor_count}")
+    result = {
+        "metric": METRIC,
+        "value": None,
+        "unit": "TFLOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, per-channel key offset N(0,0.5); no checkpoint)",
+        "config": {
+            "workload": (
+                "768p-stage streaming attention layer-call (hook NOISY step, BF16): H40 D128 "
+                f"Lq {LQ} over Lkv {LKV} = anchor {ANCHOR} + 2 x {LQ} history (cache slots, in place) "
+                f"+ {LQ} self (packed per call)"
+            ),
+            "heads": H,
+            "head_dim": D,
+            "lq": LQ,
+            "lkv": LKV,
+            "parallelism": "single GPU (heads would shard across GPUs)",
+        },
+    }
+    cache = inputs = None
+    if args.workload in ("all", "bf16", "i8qk"):
+        cache, inputs = build_stream(torch, dev, None)
+        torch.cuda.synchronize()
+    if args.workload in ("all", "bf16"):
+        wall_ms, dev_ms, comps = bench_attention(torch, dev, "sdpa", args.steps, args.warmup, cache, inputs)
+        attn_ms = comps["attention"]["mean_ms"]
+        achieved = ATTN_FLOPS / (attn_ms * 1e-3) / 1e12
+        result["value"] = round(ATTN_FLOPS / (wall_ms * 1e-3) / 1e12, 2)
+        result["ms_per_step"] = round(wall_ms, 4)
+        result["us_per_layer_call"] = round(wall_ms * 1e3, 1)
+        result["frac_bf16_peak"] = round(result["value"] / PEAK_BF16_TFLOPS, 4)
+        result["components_ms"] = {k: round(v["mean_ms"], 4) for k, v in comps.items()}
+        traffic = read_traffic()
+        result["roofline"] = {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": traffic,
+            "kernel": "attn_fwd_kernel<128, bf16>",
+            "flops_per_launch": ATTN_FLOPS,
+            "kernel_ms": round(attn_ms, 4),
+        }
+        _log(f"bf16: {wall_ms:.3f} ms/step (device {dev_ms:.3f}), kernel {attn_ms:.3f} ms = {achieved:.1f} TFLOPS")
+    if args.workload in ("all", "i8qk"):
+        wall_ms, dev_ms, comps = bench_attention(torch, dev, "sage_attn", args.steps, args.warmup, cache, inputs)
+        tflops = ATTN_FLOPS / (wall_ms * 1e-3) / 1e12
+        attn_ms = comps["attention"]["mean_ms"]
+        entry = {
+            "us_per_layer_call": round(wall_ms * 1e3, 1),
+            "tflops": round(tflops, 2),
+            "frac_bf16_peak": round(tflops / PEAK_BF16_TFLOPS, 4),
+            "frac_mixed_peak": round(tflops / (PEAK_BF16_TFLOPS * 4.0 / 3.0), 4),
+            "kernel_tflops": round(ATTN_FLOPS / (attn_ms * 1e-3) / 1e12, 2),
+            "components_ms": {k: round(v["mean_ms"], 4) for k, v in comps.items()},
+        }
+        if result["value"]:
+            entry["speedup_vs_bf16"] = round(tflops / result["value"], 3)
+        result["i8qk"] = entry
+        _log(f"i8qk: {wall_ms:.3f} ms/step, {tflops:.1f} TFLOPS, components {entry['components_ms']}")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = round(tflops, 2), round(wall_ms, 4)
+    if cache is not None:
+        del cache, inputs
+        torch.cuda.empty_cache()
+    if args.workload in ("all", "w8a8"):
+        wall_ms, dev_ms, comps = bench_w8a8(torch, dev, args.steps, args.warmup)
+        gemm_ms = comps["gemm"]["mean_ms"]
+        quant_ms = comps["token_quant"]["mean_ms"]
+        ops = 2.0 * M_X * N_W * K_X
+        qbytes = 2.0 * M_X * K_X + M_X * K_X + 4.0 * M_X
+        result["w8a8"] = {
+            "us_per_projection": round(wall_ms * 1e3, 1),
+            "gemm_us": round(gemm_ms * 1e3, 1),
+            "gemm_tops": round(ops / (gemm_ms * 1e-3) / 1e12, 2),
+            "gemm_frac_int8_peak": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+            "token_quant_us": round(quant_ms * 1e3, 1),
+            "token_quant_frac_hbm": round(qbytes / (quant_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        }
+        _log(f"w8a8: {wall_ms:.3f} ms/projection, gemm {gemm_ms:.3f} ms, quant {quant_ms:.3f} ms")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["w8a8"]["gemm_tops"], round(wall_ms, 4)
+            result["unit"] = "TOPS"
+    if not args.no_cpu_baseline and args.workload in ("all", "bf16"):
+        result["cpu_baseline"] = cpu_baseline(torch)
+        _log(f"cpu baseline: {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

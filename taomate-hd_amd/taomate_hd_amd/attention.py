@@ -14,6 +14,7 @@ from __future__ import annotations
 from typing import Any, Sequence
 
 from . import _native
+from .profiling import ComponentTimer, maybe_region
 from .slots import KV_TILE, SlotView, round_up
 
 BACKENDS = ("bf16", "i8qk")
@@ -102,6 +103,7 @@ def segment_attention(
     o_row0: int = 0,
     workspace: QKQuantWorkspace | None = None,
     return_quant: bool = False,
+    timer: ComponentTimer | None = None,
 ) -> Any:
     """Attention of the selected query rows over ``segments`` (in place, no mask).
 
@@ -168,15 +170,21 @@ def segment_attention(
     lib = _native.load()
     stream = _native.stream_ptr(torch, query.device)
     if backend == "bf16":
-        _native.check(lib.tmhd_attn_fwd_bf16(args, stream), "tmhd_attn_fwd_bf16")
+        with maybe_region(timer, "attention"):
+            status = lib.tmhd_attn_fwd_bf16(args, stream)
+        _native.check(status, "tmhd_attn_fwd_bf16")
         return out
     if workspace is None:
         workspace = QKQuantWorkspace(torch)
     qq, views = workspace.quant_struct(
         heads=heads, head_dim=head_dim, lq=lq, tokens=[s.tokens for s in segments], device=query.device
     )
-    _native.check(lib.tmhd_qk_smooth_quant(args, qq, stream), "tmhd_qk_smooth_quant")
-    _native.check(lib.tmhd_attn_fwd_i8qk(args, qq, stream), "tmhd_attn_fwd_i8qk")
+    with maybe_region(timer, "qk_quant"):
+        status = lib.tmhd_qk_smooth_quant(args, qq, stream)
+    _native.check(status, "tmhd_qk_smooth_quant")
+    with maybe_region(timer, "attention"):
+        status = lib.tmhd_attn_fwd_i8qk(args, qq, stream)
+    _native.check(status, "tmhd_attn_fwd_i8qk")
     if return_quant:
         return out, views
     return out

@@ -31,6 +31,7 @@ from typing import Any, Callable
 
 from .attention import QKQuantWorkspace, segment_attention
 from .kvcache import HeadMajorRingKVCache
+from .profiling import ComponentTimer, maybe_region
 from .slots import SlotPool, SlotView
 
 ATTENTION_BACKENDS = ("sdpa", "sage_attn")
@@ -112,6 +113,7 @@ class StreamingAttentionHook:
         attention_backend: str = "sdpa",
         condition_attention_cached: Callable[[str, int], bool] | None = None,
         compact_condition_attention_output: Callable[[str, Any], Any] | None = None,
+        timer: ComponentTimer | None = None,
     ) -> None:
         if attention_backend not in ATTENTION_BACKENDS:
             raise ValueError(f"unsupported streaming attention backend: {attention_backend}")
@@ -135,6 +137,7 @@ class StreamingAttentionHook:
         self.sage_attn_query_tokens = 0
         self.sage_attn_key_tokens = 0
         self.kernel_calls = 0
+        self.timer = timer
 
     # ---- receipts (attention_hook.py:174-191)
     def sage_attn_receipt(self) -> dict[str, Any] | None:
@@ -212,7 +215,7 @@ class StreamingAttentionHook:
             self._quant_ws = QKQuantWorkspace(torch)
         segment_attention(
             torch, query, views, scale=scale, backend=backend, out=out, workspace=self._quant_ws,
-            **q_rows.query_kwargs(), **q_rows.out_kwargs(),
+            timer=self.timer, **q_rows.query_kwargs(), **q_rows.out_kwargs(),
         )
         self.kernel_calls += 1
         if backend == "i8qk":
@@ -315,22 +318,25 @@ class StreamingAttentionHook:
         def scratch_pack(rows: _Rows) -> SlotView:
             slot = pool.acquire(rows.count)
             acquired.append(slot)
-            slot.pack(key, value, **rows.pack_kwargs())
+            with maybe_region(self.timer, "pack"):
+                slot.pack(key, value, **rows.pack_kwargs())
             return slot.view()
 
         # ---- staging first: the staged slot doubles as a K/V segment
         if self.mode is HookMode.CLEAN_COMMIT:
-            self.cache.stage(layer_name, key, value, token_tags, commit_mask)
+            with maybe_region(self.timer, "stage"):
+                self.cache.stage(layer_name, key, value, token_tags, commit_mask)
         elif fused:
             if self._fused_previous_media_indices is None:
                 p_start = boundaries[previous_live_document]
                 p_stop = boundaries[previous_live_document + 1]
                 previous_media = torch.nonzero(commit_mask[p_start:p_stop], as_tuple=False).view(-1)
                 self._fused_previous_media_indices = previous_media.add(p_start)
-            self.cache.stage(
-                layer_name, key, value, token_tags, commit_mask,
-                commit_indices=self._fused_previous_media_indices,
-            )
+            with maybe_region(self.timer, "stage"):
+                self.cache.stage(
+                    layer_name, key, value, token_tags, commit_mask,
+                    commit_indices=self._fused_previous_media_indices,
+                )
         staged_view = self.cache.staged_view(layer_name)
 
         compact = None if self._compact_output is None else self._compact_output(layer_name, query)
