@@ -224,7 +224,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8"), default="all")
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "copy"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -272,6 +272,19 @@ def main() -> int:
             "parallelism": "single GPU (heads would shard across GPUs)",
         },
     }
+    if args.workload == "copy":
+        # calibration for HBM byte counters: a plain device copy of known size
+        nbytes = 1 << 30
+        src = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=dev).normal_()
+        dst = torch.empty_like(src)
+        wall_ms, _ = time_steps(torch, lambda: dst.copy_(src), args.steps, args.warmup)
+        gbps = 2.0 * nbytes / (wall_ms * 1e-3) / 1e9
+        result.update(
+            value=round(gbps, 1), unit="GB/s", ms_per_step=round(wall_ms, 4), dtype="bf16",
+            config={"workload": f"device copy of {nbytes} bytes (reads {nbytes}, writes {nbytes})"},
+        )
+        print(json.dumps(result), flush=True)
+        return 0
     cache = inputs = None
     if args.workload in ("all", "bf16", "i8qk"):
         cache, inputs = build_stream(torch, dev, None)

@@ -1,0 +1,234 @@
+"""CPU tests of the C ABI (load, exports, struct layout) and the host logic
+(hook/session validation and state machine, W8A8 policy, slot layout)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parents[1]
+HEADER = REPO / "include" / "tmhd.h"
+
+
+def _declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(tmhd_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from taomate_hd_amd import _native
+
+    lib = _native.load()
+    declared = _declared_symbols()
+    assert len(declared) == 10
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(declared) == set(_native.EXPORTED_SYMBOLS)
+    assert _native.version().startswith("tmhd ") and "gfx950" in _native.version()
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc not available")
+def test_ctypes_structs_match_c_header(tmp_path):
+    from taomate_hd_amd import _native
+
+    src = tmp_path / "layout.c"
+    fields = {
+        "tmhd_kv_segment": [f[0] for f in _native.KVSegment._fields_],
+        "tmhd_attn_args": [f[0] for f in _native.AttnArgs._fields_],
+        "tmhd_qk_quant": [f[0] for f in _native.QKQuant._fields_],
+    }
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "tmhd.h"', "int main(void) {"]
+    for struct, names in fields.items():
+        lines.append(f'printf("{struct} %zu\\n", sizeof({struct}));')
+        for n in names:
+            lines.append(f'printf("{struct}.{n} %zu\\n", offsetof({struct}, {n}));')
+    lines += ["return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{REPO / 'include'}", str(src), "-o", str(exe)], check=True)
+    out = dict(line.rsplit(" ", 1) for line in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.splitlines())
+    for struct, cls in (("tmhd_kv_segment", _native.KVSegment), ("tmhd_attn_args", _native.AttnArgs), ("tmhd_qk_quant", _native.QKQuant)):
+        assert int(out[struct]) == ctypes.sizeof(cls), struct
+        for name in fields[struct]:
+            assert int(out[f"{struct}.{name}"]) == getattr(cls, name).offset, (struct, name)
+
+
+def test_invalid_arguments_are_rejected_without_a_gpu():
+    from taomate_hd_amd import _native
+
+    lib = _native.load()
+    args = _native.AttnArgs()
+    args.head_dim = 96
+    args.heads = 1
+    args.n_segments = 1
+    with pytest.raises(ValueError, match="head_dim"):
+        _native.check(lib.tmhd_attn_fwd_bf16(args, None), "attn")
+    with pytest.raises(ValueError, match="multiple of 64"):
+        _native.check(lib.tmhd_gemm_i8_i32(None, None, None, 4, 4, 100, 100, 100, 4, None), "gemm")
+    with pytest.raises(ValueError, match="cols"):
+        _native.check(lib.tmhd_token_quant_i8(None, None, None, 4, 12, 12, None), "quant")
+
+
+def test_vt_position_is_the_mfma_lane_order():
+    from taomate_hd_amd import vt_position
+
+    assert [vt_position(t) for t in range(16)] == [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]
+    assert all(vt_position(vt_position(t)) == t for t in range(4096))
+    # lane group g of 16-key step s reads stored columns 16s + 8g .. +7, which must hold
+    # keys 16s + 4g + {0..3} and 16s + 8 + 4g + {0..3} (the S^T accumulator rows of that lane)
+    inverse = {vt_position(t): t for t in range(64)}
+    for s in range(4):
+        for g in range(2):
+            keys = [inverse[16 * s + 8 * g + e] for e in range(8)]
+            assert keys == [16 * s + 4 * g + e for e in range(4)] + [16 * s + 8 + 4 * g + e for e in range(4)]
+
+
+def test_live_documents_resolution():
+    import torch
+
+    from taomate_hd_amd.hook import _live_documents_from_mask_or_hint
+
+    bounds = (0, 3, 3, 8, 10)
+    mask = torch.tensor([False, True, False, False, False, True, False, False, False, False])
+    assert _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=None) == (0, 2)
+    assert _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=(0, 2)) == (0, 2)
+    with pytest.raises(TypeError):
+        _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=[0])
+    with pytest.raises(ValueError, match="invalid"):
+        _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=(5,))
+    with pytest.raises(ValueError, match="sorted"):
+        _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=(2, 0))
+    with pytest.raises(ValueError, match="empty"):
+        _live_documents_from_mask_or_hint(boundaries=bounds, commit_mask=mask, live_documents_hint=(1,))
+
+
+def _hook_and_inputs():
+    import torch
+
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=("blocks.0.attn",), local_heads=2, head_dim=64))
+    hook = StreamingAttentionHook(cache)
+    q = torch.zeros(8, 2, 64, dtype=torch.bfloat16)
+    kw = dict(
+        attention=type("A", (), {"softmax_scale": 0.125})(), layer_name="blocks.0.attn", query=q, key=q, value=q,
+        token_tags=torch.zeros(8, dtype=torch.long), commit_mask=torch.ones(8, dtype=torch.bool),
+        cu_seqlens=None, cu_seqlens_host=(0, 8), max_seqlen=8,
+    )
+    return cache, hook, kw
+
+
+def test_hook_validation_and_state_machine():
+    import torch
+
+    from taomate_hd_amd import HookMode
+
+    cache, hook, kw = _hook_and_inputs()
+    with pytest.raises(RuntimeError, match="outside a streaming step"):
+        hook(**kw)
+    with pytest.raises(ValueError, match="differs from clean history"):
+        hook.activate(mode=HookMode.NOISY, block_index=1)
+    with pytest.raises(ValueError, match="fused progress-denoise"):
+        hook.activate(mode=HookMode.NOISY, block_index=0, fused_current_recent_blocks=2)
+    with pytest.raises(ValueError, match="denoise step index"):
+        hook.activate(mode=HookMode.CLEAN_COMMIT, block_index=0, denoise_step_index=0)
+    hook.activate(mode=HookMode.NOISY, block_index=0)
+    with pytest.raises(RuntimeError, match="already active"):
+        hook.activate(mode=HookMode.NOISY, block_index=0)
+    with pytest.raises(ValueError, match="non-main"):
+        hook(**{**kw, "layer_name": "blocks.9.attn"})
+    with pytest.raises(ValueError, match=r"\[tokens, 2, 64\]"):
+        hook(**{**kw, "query": torch.zeros(8, 3, 64, dtype=torch.bfloat16)})
+    with pytest.raises(ValueError, match="CUDA bfloat16"):
+        hook(**kw)  # CPU tensors: the HIP path has no CPU fallback
+    hook.deactivate()
+    with pytest.raises(ValueError):
+        type(hook)(cache, attention_backend="flash")
+
+
+def test_session_state_machine_without_gpu():
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingSession, native_stream_attention_hook
+
+    class Plan:
+        phases = ("p0", "p1")
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=("blocks.0.attn",), local_heads=2, head_dim=64))
+    with pytest.raises(TypeError):
+        StreamingSession(object())
+    session = StreamingSession(Plan(), cache=cache)
+    with pytest.raises(RuntimeError, match="context manager"):
+        with session.noisy_step(0):
+            pass
+    with session:
+        assert native_stream_attention_hook() is session.hook
+        with pytest.raises(RuntimeError, match="already installed"):
+            StreamingSession(Plan(), cache=cache).__enter__()
+        with pytest.raises(RuntimeError, match="at least one noisy"):
+            with session.clean_commit(0):
+                pass
+        with pytest.raises(ValueError, match="in order"):
+            with session.noisy_step(1):
+                pass
+        with pytest.raises(ValueError, match="unknown streaming block"):
+            session.phase(7)
+        with session.noisy_step(0) as phase:
+            assert phase == "p0" and session.hook.mode.value == "noisy"
+        assert session.hook.mode.value == "idle"
+        with pytest.raises(ValueError, match="adjacent"):
+            with session.fused_clean_commit_denoise(0, 2):
+                pass
+    assert native_stream_attention_hook() is None
+
+
+def test_cache_ledger_errors_without_gpu():
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=("blocks.0.attn",), local_heads=2, head_dim=64))
+    with pytest.raises(ValueError, match="order mismatch"):
+        cache.begin_clean_commit(1)
+    with pytest.raises(RuntimeError, match="no clean commit"):
+        cache.commit()
+    cache.begin_clean_commit(0)
+    with pytest.raises(RuntimeError, match="already active"):
+        cache.begin_clean_commit(0)
+    with pytest.raises(RuntimeError, match="during a clean commit"):
+        cache.retain_sink_and_recent_commits(2)
+    with pytest.raises(RuntimeError, match="missing attention layers"):
+        cache.commit()
+    cache.rollback()
+    assert not cache.clean_commit_active and cache.committed_blocks == 0
+    with pytest.raises(ValueError, match="non-negative"):
+        cache.retain_sink_and_recent_commits(-1)
+    with pytest.raises(KeyError):
+        cache.history("blocks.3.attn")
+    assert cache.history("blocks.0.attn") is None and cache.history_views("blocks.0.attn") == ()
+
+
+def test_w8a8_policy_hand_derived():
+    from taomate_hd_amd import resolve_h3_cutlass_w8a8_policy
+
+    names = [f"blocks.{i}.{s}" for i in range(50) for s in ("attn.qkv_proj", "attn.out_proj", "mlp.fc1", "mlp.fc2")]
+    sel = resolve_h3_cutlass_w8a8_policy(names, policy="interior_fc1_qkv_v1")
+    assert sel["bf16_boundary_block_indices"] == [0, 1, 47, 48, 49]
+    assert len(sel["quantized_linear_names"]) == 45 * 2
+    assert "blocks.2.attn.qkv_proj" in sel["quantized_linear_names"]
+    assert "blocks.46.mlp.fc1" in sel["quantized_linear_names"]
+    assert "blocks.47.mlp.fc1" in sel["bf16_protected_linear_names"]
+    assert all(not n.endswith("fc2") for n in sel["quantized_linear_names"])
+    with pytest.raises(ValueError):
+        resolve_h3_cutlass_w8a8_policy(names, policy="other")
+
+
+def test_build_recipe_targets_gfx950_without_packed_fp32():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("tmhd_build", REPO / "taomate-hd_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert "--offload-arch=gfx950" in mod.HIPCC_FLAGS
+    assert "-packed-fp32-ops" in mod.HIPCC_FLAGS

@@ -1,0 +1,285 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+The reference ships no tests, fixtures or golden vectors for this path, so
+each oracle function is pinned by closed forms, invariants, brute force on
+tiny inputs, an independent library routine, or hand-derived cases chosen so
+that a plausible mistake (dropped term, wrong sign/index, transposed operand,
+wrong rounding mode) fails.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle import bf16
+from oracle import quant as oq
+from oracle import stream as ost
+
+
+# ---------------------------------------------------------------- bf16
+def test_bf16_known_values_and_ties():
+    assert bf16.f32_to_bits(np.array([1.0], np.float32))[0] == 0x3F80
+    assert bf16.bits_to_f32(np.array([0xC040], np.uint16))[0] == -3.0
+    one_half_ulp = np.float32(1.0 + 2.0 ** -8)  # tie between 1 and 1 + 2^-7 -> even (1.0)
+    three_half = np.float32(1.0 + 3 * 2.0 ** -8)  # tie between 1+2^-7 (odd) and 1+2^-6 -> 1+2^-6
+    got = bf16.round_f32(np.array([one_half_ulp, three_half], np.float32))
+    assert got[0] == 1.0 and got[1] == np.float32(1.0 + 2.0 ** -6)
+    special = bf16.round_f32(np.array([np.inf, -np.inf, np.nan], np.float32))
+    assert np.isinf(special[0]) and special[1] < 0 and np.isnan(special[2])
+
+
+def test_bf16_roundtrip_all_patterns_and_torch_agreement():
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    vals = bf16.bits_to_f32(bits)
+    finite = np.isfinite(vals)
+    assert np.array_equal(bf16.f32_to_bits(vals[finite]), bits[finite])
+    x = np.random.default_rng(0).standard_normal(100000).astype(np.float32) * 1e3
+    want = torch.from_numpy(x).to(torch.bfloat16).float().numpy()  # torch's own RNE conversion
+    assert np.array_equal(bf16.round_f32(x), want)
+
+
+# ---------------------------------------------------------------- quantizers
+def test_token_quant_closed_forms():
+    rng = np.random.default_rng(1)
+    x = bf16.round_f32(rng.standard_normal((64, 300)).astype(np.float32))
+    x[5] = 0.0
+    q, s = oq.token_quant(x)
+    assert q.dtype == np.int8 and s.shape == (64,)
+    assert np.all(q[5] == 0) and s[5] == 0.0
+    rows = [r for r in range(64) if r != 5]
+    amax = np.abs(x[rows]).max(axis=1)
+    # the largest magnitude of every row maps to +-127
+    idx = np.abs(x[rows]).argmax(axis=1)
+    assert np.array_equal(np.abs(q[rows, idx]), np.full(len(rows), 127))
+    assert np.all(np.sign(q[rows, idx]) == np.sign(x[rows, idx]))
+    # scale = amax / 127 and dequantization error <= scale / 2
+    np.testing.assert_allclose(s[rows] * 127, amax, rtol=1e-6)
+    err = np.abs(q[rows].astype(np.float64) * s[rows, None] - x[rows])
+    assert np.all(err <= s[rows, None] * 0.5 * (1 + 1e-5))
+
+
+def test_token_quant_ties_round_half_even():
+    x = np.array([[127.0, 2.5, -3.5, 0.5, -0.5, 1.5]], np.float32)  # amax 127 -> multiplier 1.0
+    q, s = oq.token_quant(x)
+    assert q.tolist() == [[127, 2, -4, 0, 0, 2]] and s[0] == 1.0
+
+
+def test_weight_quant_closed_forms():
+    rng = np.random.default_rng(2)
+    w = bf16.round_f32((rng.standard_normal((32, 256)) * 0.02).astype(np.float32))
+    q, s = oq.weight_quant(w)
+    idx = np.abs(w).argmax(axis=1)
+    assert np.array_equal(np.abs(q[np.arange(32), idx]), np.full(32, 127))
+    assert q.min() >= -127 and q.max() <= 127
+    err = np.abs(q.astype(np.float64) * s[:, None] - w)
+    assert np.all(err <= s[:, None] * 0.5 * (1 + 1e-5))
+    # ties to even with scale exactly 1 (row max 127)
+    q2, s2 = oq.weight_quant(np.array([[127.0, -127.0, 2.5, 3.5, -0.5]], np.float32))
+    assert s2[0] == 1.0 and q2.tolist() == [[127, -127, 2, 4, 0]]
+    # the 1e-12 scale floor: amax 1e-10 would give 7.9e-13, floored to 1e-12 -> q = 100, not 127
+    tiny = np.array([[1e-10, -5e-11, 0.0]], np.float32)
+    q3, s3 = oq.weight_quant(tiny)
+    assert s3[0] == np.float32(1e-12)
+    assert q3[0, 0] == 100 and q3[0, 1] == -50
+    q4, s4 = oq.weight_quant(np.zeros((1, 8), np.float32))
+    assert s4[0] == np.float32(1e-12) and np.all(q4 == 0)
+
+
+def test_int_gemm_brute_force():
+    rng = np.random.default_rng(3)
+    a = rng.integers(-128, 128, size=(5, 70), dtype=np.int8)
+    b = rng.integers(-127, 128, size=(3, 70), dtype=np.int8)
+    a[0] = -128
+    b[0] = -127
+    want = np.zeros((5, 3), np.int64)
+    for i in range(5):
+        for j in range(3):
+            for kk in range(70):
+                want[i, j] += int(a[i, kk]) * int(b[j, kk])
+    assert np.array_equal(oq.int_gemm(a, b), want.astype(np.int32))
+    assert oq.int_gemm(a, b)[0, 0] == 128 * 127 * 70
+
+
+def test_scaled_mm_epilogue_forms():
+    acc = np.array([[3, -7], [2 ** 24 + 1, 100]], dtype=np.int32)
+    one = np.ones(2, np.float32)
+    got = oq.scaled_mm_epilogue(acc, one, one, None)
+    # int -> fp32 conversion rounds 2^24 + 1 to 2^24 before bf16 rounding
+    assert got.tolist() == [[3.0, -7.0], [2.0 ** 24, 100.0]]
+    a_s = np.array([0.5, 2.0], np.float32)
+    b_s = np.array([0.25, 4.0], np.float32)
+    got = oq.scaled_mm_epilogue(acc[:1], a_s[:1], b_s, np.array([1.0, -1.0], np.float32))
+    assert got.tolist() == [[3 * 0.25 * 0.5 + 1.0, -7 * 4.0 * 0.5 - 1.0]]
+
+
+def test_smooth_k_mean_and_block_quant():
+    k = np.full((300, 2, 4), 1.5, np.float32)
+    assert np.all(oq.smooth_k_mean(k) == 1.5)
+    k2 = np.zeros((4, 1, 1), np.float32)
+    k2[:, 0, 0] = [1, 2, 3, 4]
+    assert oq.smooth_k_mean(k2)[0, 0] == 2.5
+    rng = np.random.default_rng(4)
+    k3 = bf16.round_f32(rng.standard_normal((1000, 3, 8)).astype(np.float32))
+    m = oq.smooth_k_mean(k3)
+    # order independent and equal to the correctly rounded fp64 mean for this data
+    assert np.array_equal(m, oq.smooth_k_mean(k3[rng.permutation(1000)]))
+    assert np.array_equal(m, bf16.round_f32(k3.astype(np.float64).mean(axis=0).astype(np.float32)))
+    # blocks of 128 rows are independent; an all-zero block quantizes to zeros with scale 0
+    x = bf16.round_f32(rng.standard_normal((300, 2, 8)).astype(np.float32))
+    x[128:256] = 0.0
+    q, s = oq.block_quant(x)
+    assert s.shape == (2, 3) and np.all(s[:, 1] == 0) and np.all(q[128:256] == 0)
+    x2 = x.copy()
+    x2[290] *= 100.0
+    q2, s2 = oq.block_quant(x2)
+    assert np.array_equal(q2[:128], q[:128]) and np.array_equal(s2[:, 0], s[:, 0])
+    qa, sa = oq.token_quant(x[:128, 0, :].reshape(1, -1))  # one block of one head == one "row"
+    assert np.array_equal(q[:128, 0, :].reshape(1, -1), qa) and sa[0] == s[0, 0]
+
+
+# ---------------------------------------------------------------- attention
+def _rand(shape, seed):
+    return bf16.round_f32(np.random.default_rng(seed).standard_normal(shape).astype(np.float32))
+
+
+def test_attention_closed_forms():
+    q = _rand((7, 2, 16), 10)
+    v = _rand((9, 2, 16), 11)
+    # a single key returns its value
+    np.testing.assert_allclose(oatt.attention_fp64(q, _rand((1, 2, 16), 12), v[:1], 0.3), np.broadcast_to(v[:1], (7, 2, 16)), atol=1e-12)
+    # identical keys give the mean of the values
+    k_const = np.repeat(_rand((1, 2, 16), 13), 9, axis=0)
+    np.testing.assert_allclose(oatt.attention_fp64(q, k_const, v, 0.3), np.broadcast_to(v.mean(0), (7, 2, 16)), atol=1e-12)
+    # one dominant logit selects its value row
+    k = _rand((9, 2, 16), 14) * 0.01
+    k[4] = q[0] * 50.0
+    out = oatt.attention_fp64(q[:1], k, v, 1.0)
+    np.testing.assert_allclose(out[0], v[4], atol=1e-6)
+
+
+def test_attention_permutation_and_lse_merge():
+    q = _rand((11, 3, 32), 20)
+    k = _rand((40, 3, 32), 21)
+    v = _rand((40, 3, 32), 22)
+    s = 32 ** -0.5
+    base = oatt.attention_fp64(q, k, v, s)
+    perm = np.random.default_rng(0).permutation(40)
+    np.testing.assert_allclose(oatt.attention_fp64(q, k[perm], v[perm], s), base, atol=1e-12)
+    o1, l1 = oatt.attention_fp64(q, k[:13], v[:13], s), oatt.attention_lse_fp64(q, k[:13], s)
+    o2, l2 = oatt.attention_fp64(q, k[13:], v[13:], s), oatt.attention_lse_fp64(q, k[13:], s)
+    w1 = 1.0 / (1.0 + np.exp(l2 - l1))
+    merged = o1 * w1[..., None] + o2 * (1 - w1)[..., None]
+    np.testing.assert_allclose(merged, base, atol=1e-12)
+
+
+def test_attention_matches_torch_sdpa():
+    import torch
+
+    q = _rand((33, 2, 64), 30)
+    k = _rand((70, 2, 64), 31)
+    v = _rand((70, 2, 64), 32)
+    got = oatt.sdpa_cpu(torch.from_numpy(q), torch.from_numpy(k), torch.from_numpy(v), 0.125).numpy()
+    np.testing.assert_allclose(got, oatt.attention_fp64(q, k, v, 0.125), atol=2e-5)
+
+
+def test_i8qk_attention_algebra():
+    q = _rand((200, 2, 64), 40)
+    kseg = [_rand((150, 2, 64), 41) + 0.7, _rand((90, 2, 64), 42) - 0.3]
+    vseg = [_rand((150, 2, 64), 43), _rand((90, 2, 64), 44)]
+    out, ops = oatt.i8qk_attention(q, kseg, vseg, 0.125)
+    # dequantized operands: q ~ q_i8 * s_q, k ~ k_i8 * s_k + mean; the mean only shifts
+    # each query row's logits by a constant, which softmax removes
+    qb = np.arange(200) // 128
+    q_deq = ops["q_i8"].astype(np.float64) * ops["q_scale"].T[qb][:, :, None]
+    k_deq = []
+    for kq, ks in zip(ops["k_i8"], ops["k_scale"]):
+        kb = np.arange(kq.shape[0]) // 128
+        k_deq.append(kq.astype(np.float64) * ks.T[kb][:, :, None])
+    k_all = np.concatenate(k_deq)
+    v_all = np.concatenate(vseg)
+    np.testing.assert_allclose(oatt.attention_fp64(q_deq, k_all, v_all, 0.125), out, atol=1e-10)
+    np.testing.assert_allclose(oatt.attention_fp64(q_deq, k_all + ops["mean"][None], v_all, 0.125), out, atol=1e-10)
+    exact = oatt.attention_fp64(q, np.concatenate(kseg), v_all, 0.125)
+    assert oatt.cosine(out, exact) > 0.999
+
+
+# ---------------------------------------------------------------- stream semantics
+def test_packed_layout_hand_derived():
+    tags, mask, bounds = ost.packed_layout(3, 2, 2, 4, align=8)
+    assert tags.tolist() == [1, 1, 1, 0, 0, 2, 2, 0, 0, 0, 0] + [-1] * 5  # 11 rows aligned to 16
+    assert mask.tolist() == [False] * 5 + [True] * 6 + [False] * 5
+    assert bounds == (0, 11, 16)
+
+
+def test_cache_ledger_hand_derived():
+    layers = ("a", "b")
+    c = ost.CacheOracle(layers)
+    blocks = [(2, 2, 0, 0, 0), (0, 2, 0), (2, 0), (0, 0, 2)]
+    base = 0
+    for i, tags in enumerate(blocks):
+        n = len(tags)
+        k = np.arange(base, base + n, dtype=np.float32)[:, None, None]  # row id as the value
+        c.begin_clean_commit(i)
+        for layer in layers:
+            c.stage(layer, k, -k, np.array(tags), np.ones(n, bool))
+        c.commit()
+        c.retain_sink_and_recent_commits(2)
+        base += n
+    # after b2: sink filtered to video rows 2,3,4; after b3: b1 evicted
+    assert c.counts == [3, 2, 3]
+    assert c.tags == [(0, 0, 0), (2, 0), (0, 0, 2)]
+    assert c.history("a")[0][:, 0, 0].tolist() == [2, 3, 4, 8, 9, 10, 11, 12]
+    assert np.array_equal(c.history("b")[1], -c.history("b")[0])
+    with pytest.raises(ValueError):
+        c.begin_clean_commit(3)  # out of order
+    c.begin_clean_commit(4)
+    with pytest.raises(ValueError):
+        c.stage("a", np.zeros((2, 1, 1)), np.zeros((2, 1, 1)), np.array([0, 0]), np.ones(2, bool))  # no audio
+    c.rollback()
+
+
+def test_cache_fused_current_selection_hand_derived():
+    c = ost.CacheOracle(("a",))
+    for i, tags in enumerate([(2, 0, 0), (0, 2), (0, 0, 2, 2)]):
+        n = len(tags)
+        c.begin_clean_commit(i)
+        c.stage("a", np.full((n, 1, 1), i, np.float32), np.zeros((n, 1, 1)), np.array(tags), np.ones(n, bool))
+        c.commit()
+        if i == 1:
+            c.retain_sink_and_recent_commits(2)  # nothing evicted yet, flag set
+    # 3 blocks, sink still has audio (no retain after the third commit)
+    k = c.history_for_fused_current("a", use_sink=True, recent_blocks=2)[0][:, 0, 0]
+    assert k.tolist() == [0, 0, 2, 2, 2, 2]  # sink video rows + newest block
+    k = c.history_for_fused_current("a", use_sink=False, recent_blocks=2)[0][:, 0, 0]
+    assert k.tolist() == [2, 2, 2, 2]
+    assert c.history_for_fused_current("a", use_sink=True, recent_blocks=1)[0][:, 0, 0].tolist() == [0, 0]
+
+
+def test_hook_oracle_visibility_hand_derived():
+    rng = np.random.default_rng(7)
+    T, Hh, Dd = 10, 1, 8
+    q, k, v = (rng.standard_normal((T, Hh, Dd)).astype(np.float32) for _ in range(3))
+    tags = np.array([1, 1, 1, 2, 0, 0, 0, -1, -1, -1])
+    mask = np.array([False] * 3 + [True] * 4 + [False] * 3)
+    bounds = (0, 7, 10)
+    c = ost.CacheOracle(("a",))
+    hist_k = rng.standard_normal((5, Hh, Dd)).astype(np.float32)
+    hist_v = rng.standard_normal((5, Hh, Dd)).astype(np.float32)
+    c.history_kv["a"] = (hist_k, hist_v)
+    c.counts, c.tags, c.block_index = [5], [(2, 0, 0, 0, 0)], 1
+    h = ost.HookOracle(c)
+    h.activate("noisy", 1)
+    out = h("a", q, k, v, tags, mask, bounds, 0.5)
+    cond, media, pad = [0, 1, 2], [3, 4, 5, 6], [7, 8, 9]
+    np.testing.assert_allclose(out[cond], oatt.attention_fp64(q[cond], k[cond], v[cond], 0.5), atol=1e-12)
+    kv_k = np.concatenate([k[cond], hist_k, k[media]])
+    kv_v = np.concatenate([v[cond], hist_v, v[media]])
+    np.testing.assert_allclose(out[media], oatt.attention_fp64(q[media], kv_k, kv_v, 0.5), atol=1e-12)
+    np.testing.assert_allclose(out[pad], oatt.attention_fp64(q[pad], k[pad], v[pad], 0.5), atol=1e-12)
+    h.deactivate()
+    with pytest.raises(RuntimeError):
+        h("a", q, k, v, tags, mask, bounds, 0.5)
