@@ -31,7 +31,7 @@
 namespace tmhd {
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 8;
 constexpr int kQW = 32;            // query rows per wave
 constexpr int kBM = kWaves * kQW;  // query rows per workgroup
 constexpr int kBN = 64;            // keys per tile
@@ -101,20 +101,34 @@ __device__ __forceinline__ int xcd_logical_id(int b, int G) {
   return xcd < rem ? xcd * (per + 1) + pos : rem * (per + 1) + (xcd - rem) * per + pos;
 }
 
+// Iterator over the (segment, tile) sequence of a call.
+struct TileIt {
+  int s, t;
+  __device__ __forceinline__ void next(const KArgs &a) {
+    if (++t >= a.seg[s].ntiles) {
+      ++s;
+      t = 0;
+    }
+  }
+};
+
 template <int D, bool I8>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_kernel(const KArgs a) {
   constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row
   constexpr int KCPR = KROW / 16;       // 16-byte chunks per key row
   constexpr int KRP = 256 / KROW;       // key rows per 256 bytes (one bank sweep)
   constexpr int KT = kBN * KROW;        // key tile bytes
   constexpr int VT = D * kBN * 2;       // value tile bytes (D rows of 64 keys)
-  constexpr int KWL = KT / 1024 / kWaves;  // 1 KiB wave loads per wave per tile
-  constexpr int VWL = VT / 1024 / kWaves;
+  constexpr int NKL = KT / 1024;           // 1 KiB wave loads per key tile
+  constexpr int NVL = VT / 1024;
+  constexpr int KWL = (NKL + kWaves - 1) / kWaves;  // per wave (some waves idle if NKL < waves)
+  constexpr int VWL = (NVL + kWaves - 1) / kWaves;
   constexpr int QST = I8 ? D / 32 : D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;
-  static_assert(KWL >= 1 && VWL >= 1, "tile too small for 4 waves");
 
-  __shared__ __attribute__((aligned(1024))) char smem[2 * (KT + VT)];
+  // K and V have separate double buffers: K runs one tile ahead of V
+  __shared__ __attribute__((aligned(1024))) char kbuf[2][KT];
+  __shared__ __attribute__((aligned(1024))) char vbuf[2][VT];
 
   // chunk swizzles: 16 consecutive rows (one 16-lane ds_read_b128 phase) hit
   // 16 distinct 16-byte positions modulo 256 bytes
@@ -147,6 +161,80 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   float qscale = 1.0f;
   if constexpr (I8) qscale = a.qs[(int64_t)h * a.qshs + (qt * kBM + w * kQW) / TMHD_QUANT_BLOCK];
 
+  // per-lane byte offsets of this thread's tile loads (tile-invariant)
+  uint32_t koff[KWL], vrow[VWL], vchk[VWL];
+#pragma unroll
+  for (int i = 0; i < KWL; ++i) {
+    const int c = (w + i * kWaves) * 64 + lane, row = c / KCPR;
+    koff[i] = row * KROW + ((c % KCPR) ^ kswz(row)) * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < VWL; ++i) {
+    const int c = (w + i * kWaves) * 64 + lane, row = c >> 3;
+    vrow[i] = row;
+    vchk[i] = ((c & 7) ^ vswz(row)) * 16;
+  }
+  auto load_k = [&](TileIt it, int buf) {
+    const Seg &S = a.seg[it.s];
+    const char *base = I8 ? (const char *)(S.k8 + (int64_t)h * S.khs + (int64_t)it.t * kBN * D)
+                          : (const char *)(S.k + (int64_t)h * S.khs + (int64_t)it.t * kBN * D);
+#pragma unroll
+    for (int i = 0; i < KWL; ++i)
+      if (NKL % kWaves == 0 || w + i * kWaves < NKL)
+        load_lds16(base + koff[i], &kbuf[buf][(w + i * kWaves) * 1024]);
+  };
+  auto load_v = [&](TileIt it, int buf) {
+    const Seg &S = a.seg[it.s];
+    const char *base = (const char *)(S.vt + (int64_t)h * S.vhs + it.t * kBN);
+    const uint32_t rs = (uint32_t)S.vrs * 2;
+#pragma unroll
+    for (int i = 0; i < VWL; ++i)
+      if (NVL % kWaves == 0 || w + i * kWaves < NVL)
+        load_lds16(base + (vrow[i] * rs + vchk[i]), &vbuf[buf][(w + i * kWaves) * 1024]);
+  };
+  // S^T = K Q^T for the 64 keys of a tile: lane holds keys 32kb + 8(r/4) + 4g + r%4
+  auto qk = [&](int buf, f32x16 (&sc)[2]) {
+#pragma unroll
+    for (int kb32 = 0; kb32 < 2; ++kb32) {
+      const int krow = kb32 * 32 + lr;
+      const char *kp = &kbuf[buf][krow * KROW];
+      if constexpr (I8) {
+        i32x16 ia;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ia[r] = 0;
+#pragma unroll
+        for (int st = 0; st < QST; ++st)
+          ia = mfma_i8(*(const i32x4 *)(kp + ((2 * st + g) ^ kswz(krow)) * 16), qv[st], ia);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[kb32][r] = (float)ia[r];
+      } else {
+        f32x16 acc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+        for (int st = 0; st < QST; ++st)
+          acc = mfma_bf16(*(const i32x4 *)(kp + ((2 * st + g) ^ kswz(krow)) * 16), qv[st], acc);
+        sc[kb32] = acc;
+      }
+    }
+  };
+  auto mask_tail = [&](f32x16 (&sc)[2], int nvalid) {
+#pragma unroll
+    for (int kb32 = 0; kb32 < 2; ++kb32)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (kb32 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) sc[kb32][r] = -INFINITY;
+  };
+  auto tile_scale = [&](TileIt it) {
+    float ct = a.c;
+    if constexpr (I8) {
+      const Seg &S = a.seg[it.s];
+      // a zero-scale block must not turn a masked -inf logit into NaN
+      ct = fmaxf(a.c * qscale * S.ks[(int64_t)h * S.kshs + (it.t * kBN) / TMHD_QUANT_BLOCK], 1e-30f);
+    }
+    return ct;
+  };
+
   f32x16 o[DB];
 #pragma unroll
   for (int db = 0; db < DB; ++db)
@@ -155,84 +243,40 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
   float mref = -INFINITY;
   float lsum = 0.0f;
 
-  auto gload = [&](int s, int t, int buf) {
-    const Seg &S = a.seg[s];
-    const int t0 = t * kBN;
-    char *kd = smem + buf * (KT + VT);
-    char *vd = kd + KT;
-    const char *kg = I8 ? (const char *)(S.k8 + (int64_t)h * S.khs + (int64_t)t0 * D)
-                        : (const char *)(S.k + (int64_t)h * S.khs + (int64_t)t0 * D);
-#pragma unroll
-    for (int i = 0; i < KWL; ++i) {
-      const int blk = w * KWL + i, c = blk * 64 + lane, row = c / KCPR;
-      load_lds16(kg + row * KROW + ((c % KCPR) ^ kswz(row)) * 16, kd + blk * 1024);
-    }
-    const char *vg = (const char *)(S.vt + (int64_t)h * S.vhs + t0);
-#pragma unroll
-    for (int i = 0; i < VWL; ++i) {
-      const int blk = w * VWL + i, c = blk * 64 + lane, row = c >> 3;
-      load_lds16(vg + (int64_t)row * S.vrs * 2 + ((c & 7) ^ vswz(row)) * 16, vd + blk * 1024);
-    }
-  };
+  // ---- prologue: K(0), V(0), K(1) resident; S = scores of tile 0
+  TileIt cur{0, 0}, n1 = cur, n2;
+  n1.next(a);
+  n2 = n1;
+  if (n2.s < a.nseg) n2.next(a);
+  load_k(cur, 0);
+  load_v(cur, 0);
+  if (n1.s < a.nseg) load_k(n1, 1);
+  wait_vmem();
+  __syncthreads();
+  f32x16 sc[2];
+  qk(0, sc);
+  {
+    const int nv = a.seg[0].tokens;
+    if (nv < kBN) mask_tail(sc, nv);
+  }
+  __syncthreads();  // every wave is done with K(0) before K(2) overwrites it
 
-  auto compute = [&](int buf, int s, int t) {
-    const Seg &S = a.seg[s];
-    const char *kb = smem + buf * (KT + VT);
-    const char *vb = kb + KT;
-    const int nvalid = S.tokens - t * kBN;  // >= 1
-    const bool two = nvalid > 32;           // second 32-key block present
-    const bool partial = nvalid < kBN;
-    float ct = a.c;
-    if constexpr (I8) ct = a.c * qscale * S.ks[(int64_t)h * S.kshs + (t * kBN) / TMHD_QUANT_BLOCK];
+  for (int j = 0;; ++j) {
+    const int kb_cur = j & 1;
+    const bool has1 = n1.s < a.nseg;
+    const bool has2 = n2.s < a.nseg;
+    if (has2) load_k(n2, kb_cur);        // K(j+2) into the buffer K(j) used
+    if (has1) load_v(n1, kb_cur ^ 1);    // V(j+1) into the buffer V(j-1) used
+    const float ct = tile_scale(cur);
 
-    // S^T for keys [32*kb, 32*kb+32): lane holds keys 32kb + 8(r/4) + 4g + r%4
-    f32x16 sc[2];
-#pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32) {
-      if (kb32 == 1 && !two) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[1][r] = -INFINITY;
-        break;
-      }
-      const int krow = kb32 * 32 + lr;
-      i32x4 kk[QST];
-#pragma unroll
-      for (int st = 0; st < QST; ++st)
-        kk[st] = *(const i32x4 *)(kb + krow * KROW + ((2 * st + g) ^ kswz(krow)) * 16);
-      if constexpr (I8) {
-        i32x16 ia;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) ia[r] = 0;
-#pragma unroll
-        for (int st = 0; st < QST; ++st) ia = mfma_i8(kk[st], qv[st], ia);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[kb32][r] = (float)ia[r];
-      } else {
-        f32x16 acc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
-#pragma unroll
-        for (int st = 0; st < QST; ++st) acc = mfma_bf16(kk[st], qv[st], acc);
-        sc[kb32] = acc;
-      }
-    }
-    // masked keys of a partial tile
-    if (partial) {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (kb32 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) sc[kb32][r] = -INFINITY;
-    }
+    // online softmax of tile j (log2 units, lazy rescale)
     float m = sc[0][0];
 #pragma unroll
     for (int r = 1; r < 16; ++r) m = fmaxf(m, sc[0][r]);
 #pragma unroll
     for (int r = 0; r < 16; ++r) m = fmaxf(m, sc[1][r]);
     m = fmaxf(m, __shfl_xor(m, 32));
-    // masked logits stay -inf after scaling only if ct > 0; a zero INT8 block
-    // (ct == 0) must not turn -inf * 0 into NaN
-    const float cand = m == -INFINITY ? -INFINITY : m * ct;
+    const float cand = m * ct;
     if (__any(cand > mref + kLazyRescale)) {
       const float mn = fmaxf(mref, cand);
       const float alpha = (mref == -INFINITY) ? 0.0f : __builtin_amdgcn_exp2f(mref - mn);
@@ -246,61 +290,47 @@ __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))
     const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
     for (int kb32 = 0; kb32 < 2; ++kb32) {
-      if (kb32 == 1 && !two) break;
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        float p0 = __builtin_amdgcn_exp2f(fmaf(sc[kb32][r], ct, nm));
-        float p1 = __builtin_amdgcn_exp2f(fmaf(sc[kb32][r + 1], ct, nm));
-        if constexpr (I8) {
-          if (partial) {  // -inf * 0 guard for zero-scale blocks
-            p0 = sc[kb32][r] == -INFINITY ? 0.0f : p0;
-            p1 = sc[kb32][r + 1] == -INFINITY ? 0.0f : p1;
-          }
-        }
-        pk[kb32][r >> 1] = pack_bf16x2(p0, p1);
-      }
+      for (int r = 0; r < 16; r += 2)
+        pk[kb32][r >> 1] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(sc[kb32][r], ct, nm)),
+                                       __builtin_amdgcn_exp2f(fmaf(sc[kb32][r + 1], ct, nm)));
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pk[kb32][i]), ones, lsum, false);
     }
-    // O^T += V^T P^T, 16 keys per MFMA
+    // scores of tile j+1 (independent of the softmax above: overlappable).
+    // Computed unconditionally so that this block stays one scheduling
+    // region; after the last tile it reads a stale (in-bounds) buffer and
+    // the result is dropped.
+    f32x16 sn[2];
+    qk(kb_cur ^ 1, sn);
+    // O^T += V^T P^T for tile j, 16 keys per MFMA
 #pragma unroll
     for (int kb32 = 0; kb32 < 2; ++kb32) {
-      if (kb32 == 1 && !two) break;
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const i32x4 pb = {(int)pk[kb32][4 * st], (int)pk[kb32][4 * st + 1], (int)pk[kb32][4 * st + 2],
                           (int)pk[kb32][4 * st + 3]};
 #pragma unroll
         for (int db = 0; db < DB; ++db) {
-          const int vrow = db * 32 + lr;
-          const i32x4 vv = *(const i32x4 *)(vb + vrow * 128 + ((4 * kb32 + 2 * st + g) ^ vswz(vrow)) * 16);
+          const int vrow_ = db * 32 + lr;
+          const i32x4 vv = *(const i32x4 *)(&vbuf[kb_cur][vrow_ * 128 + ((4 * kb32 + 2 * st + g) ^ vswz(vrow_)) * 16]);
           o[db] = mfma_bf16(vv, pb, o[db]);
         }
       }
     }
-  };
-
-  // ---- key/value tile loop over the segment table
-  int s = 0, t = 0, buf = 0;
-  gload(s, t, 0);
-  wait_vmem();
-  __syncthreads();
-  for (;;) {
-    int ns = s, nt = t + 1;
-    if (nt >= a.seg[s].ntiles) {
-      ns = s + 1;
-      nt = 0;
+    if (!has1) break;
+    {
+      const int nv = a.seg[n1.s].tokens - n1.t * kBN;
+      if (nv < kBN) mask_tail(sn, nv);
     }
-    const bool has_next = ns < a.nseg;
-    if (has_next) gload(ns, nt, buf ^ 1);
-    compute(buf, s, t);
-    if (!has_next) break;
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+    cur = n1;
+    n1 = n2;
+    if (has2) n2.next(a);
     wait_vmem();
     __syncthreads();
-    buf ^= 1;
-    s = ns;
-    t = nt;
   }
 
   // ---- epilogue: O = O^T / l, written token-major (4 consecutive d per store)
@@ -403,9 +433,9 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   if (grid > 0x7fffffff) return set_error(TMHD_ERR_UNSUPPORTED, "attention: grid too large");
   hipStream_t s = (hipStream_t)stream;
   if (args->head_dim == 128)
-    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3((unsigned)grid), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, k);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3((unsigned)grid), dim3(256), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, k);
   return check_launch(I8 ? "tmhd_attn_fwd_i8qk" : "tmhd_attn_fwd_bf16");
 }
 
