@@ -91,23 +91,51 @@ __device__ __forceinline__ int64_t to_fixed(float x) {
   return (int64_t)__builtin_rintf(y);
 }
 
-// grid (ceil(tokens / 1024), H); thread (d = tid % D, part = tid / D)
+// Fixed-point column sums of one head's keys over 256 tokens per workgroup.
+// Thread (c, r) reads 16-byte chunk c (8 channels) of rows t0 + r, t0 + r + RPI, ...
+// and keeps 8 int64 partial sums; partials are combined in LDS and added to
+// ws[h][d] with one 64-bit atomic per channel.  Values with |x| < 127 take the
+// int32 conversion path; a chunk holding a larger value takes the int64 path
+// (both give rint(x * 2^24) exactly).
 template <int D>
 __global__ void __launch_bounds__(256) k_sum_kernel(const uint16_t *__restrict__ k, int64_t khs, int32_t tokens,
                                                     int64_t *__restrict__ ws) {
-  constexpr int PARTS = 256 / D;
-  __shared__ long long part_sum[256];
-  const int h = blockIdx.y, tid = threadIdx.x, d = tid % D, part = tid / D;
-  const int t0 = blockIdx.x * 1024;
-  const int t1 = min(t0 + 1024, tokens);
-  const uint16_t *base = k + (int64_t)h * khs + d;
-  long long acc = 0;
-  for (int t = t0 + part; t < t1; t += PARTS) acc += to_fixed(bf16_bits_to_f32(base[(int64_t)t * D]));
-  part_sum[tid] = acc;
+  constexpr int CPR = D / 8;      // 16-byte chunks per row
+  constexpr int RPI = 256 / CPR;  // rows per pass
+  __shared__ long long part[RPI][D];
+  const int h = blockIdx.y, tid = threadIdx.x, c = tid % CPR, r = tid / CPR;
+  const int t0 = blockIdx.x * 256;
+  const int t1 = min(t0 + 256, tokens);
+  const uint16_t *base = k + (int64_t)h * khs + c * 8;
+  long long acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0;
+  for (int t = t0 + r; t < t1; t += RPI) {
+    const i32x4 raw = *(const i32x4 *)(base + (int64_t)t * D);
+    float x[8];
+    float mx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[2 * e] = bf16_bits_to_f32((uint32_t)raw[e] & 0xffffu);
+      x[2 * e + 1] = bf16_bits_to_f32((uint32_t)raw[e] >> 16);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[e]));
+    if (mx < 127.0f) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += (long long)(int)__builtin_rintf(x[e] * 16777216.0f);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += to_fixed(x[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) part[r][c * 8 + e] = acc[e];
   __syncthreads();
-  if (part == 0) {
-    for (int p = 1; p < PARTS; ++p) acc += part_sum[p * D + d];
-    atomicAdd((unsigned long long *)(ws + h * D + d), (unsigned long long)acc);
+  if (tid < D) {
+    long long sum = 0;
+    for (int i = 0; i < RPI; ++i) sum += part[i][tid];
+    atomicAdd((unsigned long long *)(ws + h * D + tid), (unsigned long long)sum);
   }
 }
 
@@ -205,7 +233,7 @@ int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s
   hipLaunchKernelGGL(zero_i64_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, H * D);
   for (int i = 0; i < a->n_segments; ++i) {
     const tmhd_kv_segment &sg = a->seg[i];
-    hipLaunchKernelGGL(k_sum_kernel<D>, dim3((sg.tokens + 1023) / 1024, H), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_sum_kernel<D>, dim3((sg.tokens + 255) / 256, H), dim3(256), 0, s,
                        (const uint16_t *)sg.k, sg.k_head_stride, sg.tokens, qq->mean_workspace);
   }
   hipLaunchKernelGGL(k_mean_finalize_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace,

@@ -122,11 +122,17 @@ int launch_row_quant(int8_t *q, float *scale, const void *x, int32_t rows, int32
 
 // ---------------------------------------------------------------------------
 // INT8 GEMM: C[m][n] = sum_k A[m][k] * B[n][k] with v_mfma_i32_32x32x32_i8.
-// Workgroup tile 256 x 256 (4 waves of 128 x 128), k-tile 64, double-buffered
-// LDS.  LDS rows are 64 bytes (4 chunks of 16); chunk c of row r is stored at
-// c ^ ((r >> 1) & 3) so the 8 lanes of one ds_read_b128 phase hit 8 distinct
-// 16-byte bank groups.
-constexpr int GBM = 256, GBN = 256, GBK = 64;
+// Workgroup tile 256 (m) x 256 (n), 8 waves as 4 (m) x 2 (n), each wave
+// 64 x 128 (128 int32 accumulators per lane, two waves per SIMD).  The MFMA
+// computes the transposed block D[n][m] = B-rows x A-rows, so a lane holds
+// four consecutive n of one m and writes 4 bf16 (8 bytes) at a time.
+// k-tiles of 64 stream through a 3-deep LDS ring filled by
+// global_load_lds_dwordx4; the loop is unrolled by the ring depth so every
+// LDS address is a compile-time slot.  LDS rows are 64 bytes (4 chunks);
+// chunk c of row r sits at c ^ ((r >> 2) & 3), so the 16 lanes of one
+// ds_read_b128 phase hit 16 distinct 16-byte bank groups.
+constexpr int GBM = 256, GBN = 256, GBK = 64, GWAVES = 8, GRING = 3;
+constexpr int GSTAGE = (GBM + GBN) * GBK;  // bytes per ring slot
 
 struct GArgs {
   const int8_t *a;
@@ -145,12 +151,17 @@ __device__ __forceinline__ int xcd_logical_id(int b, int G) {
   return xcd < rem ? xcd * (per + 1) + pos : rem * (per + 1) + (xcd - rem) * per + pos;
 }
 
+__device__ __forceinline__ void load_lds16(const void *gptr, void *lds) {
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+}
+
 template <bool RAW>
-__global__ void __launch_bounds__(256, 1) gemm_i8_kernel(const GArgs ga) {
+__global__ void __launch_bounds__(GWAVES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+gemm_i8_kernel(const GArgs ga) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(16))) char smem[2 * (GBM + GBN) * GBK];
+  __shared__ __attribute__((aligned(1024))) char smem[GRING][GSTAGE];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, lr = lane & 31, g = lane >> 5;
-  const int wm = w >> 1, wn = w & 1;
+  const int wm = w >> 1, wn = w & 1;  // wave tile: a rows [wm*64, +64), b rows [wn*128, +128)
   // grouped tile order: 8 row tiles share each column sweep (L2 reuse)
   const int L = xcd_logical_id(blockIdx.x, gridDim.x);
   constexpr int GROUP = 8;
@@ -162,99 +173,122 @@ __global__ void __launch_bounds__(256, 1) gemm_i8_kernel(const GArgs ga) {
   const int tn = (L % per_group) / gsize;
   const int m0 = tm * GBM, n0 = tn * GBN;
 
-  i32x16 acc[4][4];
+  // loads: the a tile (256 rows x 64 B) and b tile are 16 wave loads each; wave w
+  // loads blocks w and w + 8 of each (16 rows of 64 B per 1 KiB block)
+  const int8_t *asrc[2];
+  const int8_t *bsrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int blk = w + i * GWAVES, row = blk * 16 + (lane >> 2), ch = (lane & 3) ^ ((row >> 2) & 3);
+    asrc[i] = ga.a + (int64_t)min(m0 + row, ga.m - 1) * ga.lda + ch * 16;
+    bsrc[i] = ga.b + (int64_t)min(n0 + row, ga.n - 1) * ga.ldb + ch * 16;
+  }
+  auto issue = [&](int kt, char *slot) {
+    const int k0 = kt * GBK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      load_lds16(asrc[i] + k0, slot + (w + i * GWAVES) * 1024);
+      load_lds16(bsrc[i] + k0, slot + GBM * GBK + (w + i * GWAVES) * 1024);
+    }
+  };
+  // per-lane LDS byte offsets of the MFMA operands (k-step 0; k-step 1 flips chunk bit 1)
+  const int arow0 = wm * 64 + lr, brow0 = wn * 128 + lr;
+  const int aoff = arow0 * 64 + ((g ^ ((arow0 >> 2) & 3)) * 16);
+  const int boff = GBM * GBK + brow0 * 64 + ((g ^ ((brow0 >> 2) & 3)) * 16);
+
+  i32x16 acc[4][2];  // [n block][m block], D[n][m]
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  i32x4 ra[4], rb[4];
-  const int8_t *arow[4];
-  const int8_t *brow[4];
-  int lpos[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = i * 256 + tid, row = c >> 2, ch = c & 3;
-    arow[i] = ga.a + (int64_t)min(m0 + row, ga.m - 1) * ga.lda + ch * 16;
-    brow[i] = ga.b + (int64_t)min(n0 + row, ga.n - 1) * ga.ldb + ch * 16;
-    lpos[i] = (row * 4 + (ch ^ ((row >> 1) & 3))) * 16;
-  }
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ra[i] = *(const i32x4 *)(arow[i] + k0);
-      rb[i] = *(const i32x4 *)(brow[i] + k0);
-    }
-  };
-  auto lstore = [&](int buf) {
-    char *sa = smem + buf * (GBM + GBN) * GBK;
-    char *sb = sa + GBM * GBK;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(i32x4 *)(sa + lpos[i]) = ra[i];
-      *(i32x4 *)(sb + lpos[i]) = rb[i];
-    }
-  };
-  auto compute = [&](int buf) {
-    const char *sa = smem + buf * (GBM + GBN) * GBK;
-    const char *sb = sa + GBM * GBK;
+  auto compute = [&](const char *slot) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      i32x4 av[4], bv[4];
+      // keep each k-step's operand reads next to its MFMAs (bounds register pressure)
+      __builtin_amdgcn_sched_barrier(0);
+      // chunk (2*ks + g) ^ sw == (g ^ sw) ^ (2*ks): k-step 1 toggles byte offset bit 5
+      i32x4 av[2], bv[4];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int off = aoff + j * 32 * 64;
+        av[j] = *(const i32x4 *)(slot + (off ^ (ks * 32)));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int ar = wm * 128 + i * 32 + lr, br = wn * 128 + i * 32 + lr;
-        av[i] = *(const i32x4 *)(sa + (ar * 4 + ((2 * ks + g) ^ ((ar >> 1) & 3))) * 16);
-        bv[i] = *(const i32x4 *)(sb + (br * 4 + ((2 * ks + g) ^ ((br >> 1) & 3))) * 16);
+        const int off = boff + i * 32 * 64;
+        bv[i] = *(const i32x4 *)(slot + (off ^ (ks * 32)));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av[i], bv[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bv[i], av[j], acc[i][j], 0, 0, 0);
     }
   };
 
   const int nk = ga.k / GBK;
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  int buf = 0;
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool has_next = kt + 1 < nk;
-    if (has_next) gload((kt + 1) * GBK);
-    compute(buf);
-    if (!has_next) break;
-    lstore(buf ^ 1);
+  issue(0, smem[0]);
+  if (nk > 1) issue(1, smem[1]);
+  // iteration kt: stage kt ready (wait), everyone past iteration kt-1 (barrier),
+  // refill the slot freed by kt-1 with stage kt+2, compute stage kt
+  auto step = [&](int kt, char *cur, char *fill) {
+    if (kt + 1 < nk)
+      __builtin_amdgcn_s_waitcnt(0x0f74);  // vmcnt(4): stage kt+1's 4 loads may stay in flight
+    else
+      __builtin_amdgcn_s_waitcnt(0x0f70);
     __syncthreads();
-    buf ^= 1;
+    if (kt + 2 < nk) issue(kt + 2, fill);
+    compute(cur);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // one exit only: the accumulators keep their registers across the unrolled steps
+  int kt = 0;
+  for (; kt + GRING <= nk; kt += GRING) {
+    step(kt, smem[0], smem[2]);
+    step(kt + 1, smem[1], smem[0]);
+    step(kt + 2, smem[2], smem[1]);
   }
+  if (kt < nk) step(kt, smem[0], smem[2]);
+  if (kt + 1 < nk) step(kt + 1, smem[1], smem[0]);
 
-  // epilogue: lane holds column n = lr of each 32x32 block, rows 8*(r/4)+4*g+r%4
+  // epilogue: lane holds m = m-block base + lr; n = n-block base + 8u + 4g + (0..3)
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 128 + j * 32 + lr;
-    if (n >= ga.n) continue;
-    float bsn = 0.0f, biasn = 0.0f;
-    if constexpr (!RAW) {
-      bsn = ga.bs[n];
-      if (ga.bias) biasn = bf16_bits_to_f32(ga.bias[n]);
-    }
+  for (int j = 0; j < 2; ++j) {
+    const int m = m0 + wm * 64 + j * 32 + lr;
+    if (m >= ga.m) continue;
+    const float asm_ = RAW ? 0.0f : ga.as[m];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (m < ga.m) {
-          if constexpr (RAW) {
-            ((int32_t *)ga.out)[(int64_t)m * ga.ldo + n] = acc[i][j][r];
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
+        if (n >= ga.n) continue;
+        if constexpr (RAW) {
+          int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
+          if (n + 3 < ga.n) {
+            *(i32x4 *)op = i32x4{acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
           } else {
-            float t = (float)acc[i][j][r];
-            t = t * bsn;
-            t = t * ga.as[m];
-            if (ga.bias) t = t + biasn;
-            ((uint16_t *)ga.out)[(int64_t)m * ga.ldo + n] = f32_to_bf16_bits(t);
+            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[i][j][4 * u + e];
+          }
+        } else {
+          uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+          uint16_t vals[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int nn = min(n + e, ga.n - 1);
+            float t = (float)acc[i][j][4 * u + e];
+            t = t * ga.bs[nn];
+            t = t * asm_;
+            if (ga.bias) t = t + bf16_bits_to_f32(ga.bias[nn]);
+            vals[e] = f32_to_bf16_bits(t);
+          }
+          if (n + 3 < ga.n) {
+            *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                                 (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+          } else {
+            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
           }
         }
       }
@@ -274,7 +308,7 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
   if (m == 0) return TMHD_OK;
   GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + GBM - 1) / GBM, (n + GBN - 1) / GBN};
   const int64_t grid = (int64_t)ga.tm_count * ga.tn_count;
-  hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, ga);
+  hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(GWAVES * 64), 0, (hipStream_t)stream, ga);
   return check_launch(what);
 }
 
