@@ -8,19 +8,21 @@
 // order and never concatenated.
 //
 // Work decomposition
-//   workgroup = 8 waves = 256 query rows of one head (one workgroup per CU,
-//   two waves per SIMD); each wave owns 32 query rows and keeps them, their
-//   fp32 output accumulators and the online-softmax state in registers
-//   (<= 256 VGPRs).  Keys stream through LDS in 64-token tiles loaded with
-//   global_load_lds_dwordx4 (no VGPR staging); K runs two tiles ahead of the
-//   tile being finished and V one tile ahead, each double-buffered.
+//   workgroup = 4 waves = 256 query rows of one head, one workgroup per CU and
+//   one wave per SIMD.  Each wave owns 64 query rows (two 32-row halves) and
+//   keeps their query operands and fp32 output accumulators in AGPRs at fixed
+//   registers, the scores, probabilities and online-softmax state in VGPRs.
+//   Keys and values stream through LDS in 64-token tiles, triple-buffered
+//   (tile t in buffer t % 3) and loaded with global_load_lds_dwordx4 (no
+//   VGPR staging): K runs two tiles ahead of the tile being finished, V one.
 //   Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16
 //   (or v_mfma_i32_32x32x32_i8), so each lane holds 16 keys of one query
 //   column; the same registers, exponentiated and converted to bf16, are
 //   directly the B operand of O^T += V^T P^T.  The value slot layout
 //   (transposed, 4-token chunks interleaved) makes the matching A operand one
-//   16-byte LDS read.  LDS rows are XOR-swizzled per 16-byte chunk so that
-//   each 16-lane phase of a ds_read_b128 touches 16 distinct bank groups.
+//   16-byte LDS read.  LDS rows are padded to an odd number of 16-byte chunks
+//   so that each 16-lane phase of a ds_read_b128 touches 16 distinct bank
+//   groups and every operand read is one base register plus an immediate.
 //
 // Softmax in log2 units with a folded reference
 //   BF16: the query is pre-scaled by scale*log2(e) (rounded to bf16 once) and
@@ -32,12 +34,14 @@
 //   The reference m only moves (and O, l are rescaled) when a tile's score
 //   exceeds it by 2^8 (lazy rescale); P values stay <= 2^8.
 //
-// One loop iteration (tile j) is one basic block scheduled explicitly:
-//   exp2 / pack / row-sum of P(j)        interleaved with QK(j+1)'s MFMAs,
-//   max of S(j+1)                        interleaved with PV(j)'s MFMAs,
-//   LDS operand reads issued two MFMAs ahead.
-//   Rare work (partial tiles, rescale, segment switches) sits in branches
-//   after the block.
+// Pipeline: a tile is two 32-key sub-tiles; each sub-tile is one basic block
+// of fenced slots, each slot one LDS operand read (issued three slots ahead)
+// and two MFMAs (one per query half) plus its share of VALU work:
+//   exp2 / pack / row-sum of P(s)      under the score MFMAs of sub-tile s+1,
+//   scaling and row max of S(s+1)      under the P.V MFMAs of sub-tile s,
+//   the tile loads of the iteration    in the first sub-tile's slots.
+// The last slots read the first operands of the next sub-tile.  Rare work
+// (partial tiles, rescale, segment switches) sits in branches after the block.
 #include <math.h>
 
 #include <type_traits>
@@ -47,20 +51,14 @@
 namespace tmhd {
 namespace {
 
-constexpr int kWaves = 8;
-constexpr int kQW = 32;            // query rows per wave
+constexpr int kWaves = 4;
+constexpr int kQW = 64;            // query rows per wave (two 32-row halves)
 constexpr int kBM = kWaves * kQW;  // query rows per workgroup
 constexpr int kBN = 64;            // keys per tile
 constexpr float kLazyRescale = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kI8Magic = 0x4B400000;  // bits of 1.5 * 2^23
 constexpr float kI8MagicF = 12582912.0f;
-
-// sched_group_barrier instruction classes
-constexpr int kSgMfma = 0x008;
-constexpr int kSgValu = 0x002;
-constexpr int kSgTrans = 0x400;
-constexpr int kSgDsRead = 0x100;
 
 struct Seg {
   const uint16_t *k;
@@ -95,31 +93,9 @@ struct KArgs {
   Seg seg[kMaxSeg];
 };
 
-__device__ __forceinline__ f32x16 mfma_bf16(i32x4 a, i32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
-                                                 __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ i32x16 mfma_i8(i32x4 a, i32x4 b, i32x16 c) {
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   bf16x2 v = {(__bf16)a, (__bf16)b};
   return __builtin_bit_cast(uint32_t, v);
-}
-
-// 16 bytes global -> LDS without a VGPR round trip.  `lds` is the wave's
-// 1 KiB destination block; lane i's bytes land at lds + 16 * i.
-// Issued as inline asm on purpose: the compiler's wait-count insertion cannot
-// tell the destination block from the tiles being read and would place a
-// vmcnt(0) wait in front of the next LDS read, serialising the prefetch.  The
-// kernel itself waits (vmcnt(0) + barrier) before any read of a loaded tile;
-// extra in-order vector-memory operations unknown to the compiler only make
-// its own vmcnt waits stricter.
-__device__ __forceinline__ void load_lds16(const void *gptr, void *lds) {
-  const uint32_t m0v = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void *)lds;
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(gptr), "{m0}"(m0v) : "memory");
 }
 
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0)
@@ -170,8 +146,197 @@ __device__ __forceinline__ void stream_next(Stream &S, const KArgs &a, int h) {
   }
 }
 
+// ---- MFMA wrappers.  All MFMAs of the kernel are inline asm so that the
+// query operands and the output accumulators can live in AGPRs (1 wave per
+// SIMD, up to 512 registers) while scores and probabilities stay in VGPRs.
+// The compiler does not see through the asm, so the hazards it would resolve
+// for builtins are resolved by construction in the kernel:
+//   * VALU write -> MFMA operand read needs 2 wait states: the first MFMA that
+//     reads a freshly packed P group uses the *_fresh form (s_nop 1);
+//   * MFMA result -> VALU read (12 wait states for either MFMA): score results
+//     are first read one slot (two MFMAs) plus 16 wait states after the last
+//     score MFMA; AGPR accumulators are read only after mfma_drain();
+//   * accvgpr write (rescale) -> MFMA accumulate: s_nop 2 after the rescale;
+//   * the rescale itself reads each AGPR after mfma_drain();
+//   * back-to-back accumulation into the same registers needs no wait states.
+// Output registers of the first MFMA of a score chain are early-clobber, so
+// they never overlap the operands.
+// Query operand block qb (4 dwords per lane) lives in the fixed AGPRs
+// a[128 + 4 qb, 128 + 4 qb + 3]; the score MFMAs name that range.
+#define TMHD_QBLK(QB, LO, HI)                                                                                \
+  case QB:                                                                                                   \
+    asm volatile("" : "+{a[" #LO ":" #HI "]}"(q));                                                           \
+    break;
+__device__ __forceinline__ void qpin(int qb, i32x4 &q) {
+  switch (qb) {
+    TMHD_QBLK(0, 128, 131)
+    TMHD_QBLK(1, 132, 135)
+    TMHD_QBLK(2, 136, 139)
+    TMHD_QBLK(3, 140, 143)
+    TMHD_QBLK(4, 144, 147)
+    TMHD_QBLK(5, 148, 151)
+    TMHD_QBLK(6, 152, 155)
+    TMHD_QBLK(7, 156, 159)
+    TMHD_QBLK(8, 160, 163)
+    TMHD_QBLK(9, 164, 167)
+    TMHD_QBLK(10, 168, 171)
+    TMHD_QBLK(11, 172, 175)
+    TMHD_QBLK(12, 176, 179)
+    TMHD_QBLK(13, 180, 183)
+    TMHD_QBLK(14, 184, 187)
+    TMHD_QBLK(15, 188, 191)
+  }
+}
+#undef TMHD_QBLK
+#define TMHD_QBLK(QB, LO, HI)                                                                                      \
+  case QB:                                                                                                         \
+    if (first)                                                                                                     \
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "v"(c));       \
+    else                                                                                                           \
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q));                \
+    break;
+// S^T (+)= K Q^T for one k-step: `first` starts the chain at c.
+__device__ __forceinline__ void qk_bf16(int qb, bool first, f32x16 &d, i32x4 k, const i32x4 &q, const f32x16 &c) {
+  switch (qb) {
+    TMHD_QBLK(0, 128, 131)
+    TMHD_QBLK(1, 132, 135)
+    TMHD_QBLK(2, 136, 139)
+    TMHD_QBLK(3, 140, 143)
+    TMHD_QBLK(4, 144, 147)
+    TMHD_QBLK(5, 148, 151)
+    TMHD_QBLK(6, 152, 155)
+    TMHD_QBLK(7, 156, 159)
+    TMHD_QBLK(8, 160, 163)
+    TMHD_QBLK(9, 164, 167)
+    TMHD_QBLK(10, 168, 171)
+    TMHD_QBLK(11, 172, 175)
+    TMHD_QBLK(12, 176, 179)
+    TMHD_QBLK(13, 180, 183)
+    TMHD_QBLK(14, 184, 187)
+    TMHD_QBLK(15, 188, 191)
+  }
+}
+#undef TMHD_QBLK
+#define TMHD_QBLK(QB, LO, HI)                                                                                      \
+  case QB:                                                                                                         \
+    if (first)                                                                                                     \
+      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "v"(c));         \
+    else                                                                                                           \
+      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q));                  \
+    break;
+// INT8 form: the chain starts at the accumulator vector c.
+__device__ __forceinline__ void qk_i8(int qb, bool first, i32x16 &d, i32x4 k, const i32x4 &q, const i32x16 &c) {
+  switch (qb) {
+    TMHD_QBLK(0, 128, 131)
+    TMHD_QBLK(1, 132, 135)
+    TMHD_QBLK(2, 136, 139)
+    TMHD_QBLK(3, 140, 143)
+    TMHD_QBLK(4, 144, 147)
+    TMHD_QBLK(5, 148, 151)
+    TMHD_QBLK(6, 152, 155)
+    TMHD_QBLK(7, 156, 159)
+    TMHD_QBLK(8, 160, 163)
+    TMHD_QBLK(9, 164, 167)
+    TMHD_QBLK(10, 168, 171)
+    TMHD_QBLK(11, 172, 175)
+    TMHD_QBLK(12, 176, 179)
+    TMHD_QBLK(13, 180, 183)
+    TMHD_QBLK(14, 184, 187)
+    TMHD_QBLK(15, 188, 191)
+  }
+}
+#undef TMHD_QBLK
+// Output accumulator block b (16 fp32 per lane) lives in the fixed AGPRs
+// a[16b, 16b + 15] for the whole kernel: every asm that touches it names that
+// range, so the compiler never moves it, and the rare rescale can address the
+// registers by name.
+#define TMHD_OBLK(B, LO, HI)                                                                         \
+  case B:                                                                                            \
+    if (fresh)                                                                                       \
+      asm("s_nop 1\n\tv_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+{a[" #LO ":" #HI "]}"(o) : "v"(v), "v"(p)); \
+    else                                                                                             \
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+{a[" #LO ":" #HI "]}"(o) : "v"(v), "v"(p));    \
+    break;
+__device__ __forceinline__ void pv(int b, bool fresh, f32x16 &o, i32x4 v, i32x4 p) {
+  switch (b) {
+    TMHD_OBLK(0, 0, 15)
+    TMHD_OBLK(1, 16, 31)
+    TMHD_OBLK(2, 32, 47)
+    TMHD_OBLK(3, 48, 63)
+    TMHD_OBLK(4, 64, 79)
+    TMHD_OBLK(5, 80, 95)
+    TMHD_OBLK(6, 96, 111)
+    TMHD_OBLK(7, 112, 127)
+  }
+}
+#undef TMHD_OBLK
+// Declares block b as live in its AGPRs at this point (after C++ code wrote
+// it, or before C++ code reads it).
+#define TMHD_OPIN(B, LO, HI) \
+  case B:                    \
+    asm volatile("" : "+{a[" #LO ":" #HI "]}"(o)); \
+    break;
+__device__ __forceinline__ void opin(int b, f32x16 &o) {
+  switch (b) {
+    TMHD_OPIN(0, 0, 15)
+    TMHD_OPIN(1, 16, 31)
+    TMHD_OPIN(2, 32, 47)
+    TMHD_OPIN(3, 48, 63)
+    TMHD_OPIN(4, 64, 79)
+    TMHD_OPIN(5, 80, 95)
+    TMHD_OPIN(6, 96, 111)
+    TMHD_OPIN(7, 112, 127)
+  }
+}
+#undef TMHD_OPIN
+// o *= alpha for block b, in place in its AGPRs (read, multiply, write back).
+#define TMHD_RS(N) "v_accvgpr_read_b32 %1, a" #N "\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 a" #N ", %1\n\t"
+#define TMHD_RS4(A, B, C, D) TMHD_RS(A) TMHD_RS(B) TMHD_RS(C) TMHD_RS(D)
+#define TMHD_ORS(B, LO, HI, R0, R1, R2, R3)                                                  \
+  case B:                                                                                    \
+    asm volatile(R0 R1 R2 R3 : "+{a[" #LO ":" #HI "]}"(o), "=&v"(t) : "v"(alpha) : "memory"); \
+    break;
+__device__ __forceinline__ void orescale(int b, f32x16 &o, float alpha) {
+  float t;
+  switch (b) {
+    TMHD_ORS(0, 0, 15, TMHD_RS4(0, 1, 2, 3), TMHD_RS4(4, 5, 6, 7), TMHD_RS4(8, 9, 10, 11), TMHD_RS4(12, 13, 14, 15))
+    TMHD_ORS(1, 16, 31, TMHD_RS4(16, 17, 18, 19), TMHD_RS4(20, 21, 22, 23), TMHD_RS4(24, 25, 26, 27),
+             TMHD_RS4(28, 29, 30, 31))
+    TMHD_ORS(2, 32, 47, TMHD_RS4(32, 33, 34, 35), TMHD_RS4(36, 37, 38, 39), TMHD_RS4(40, 41, 42, 43),
+             TMHD_RS4(44, 45, 46, 47))
+    TMHD_ORS(3, 48, 63, TMHD_RS4(48, 49, 50, 51), TMHD_RS4(52, 53, 54, 55), TMHD_RS4(56, 57, 58, 59),
+             TMHD_RS4(60, 61, 62, 63))
+    TMHD_ORS(4, 64, 79, TMHD_RS4(64, 65, 66, 67), TMHD_RS4(68, 69, 70, 71), TMHD_RS4(72, 73, 74, 75),
+             TMHD_RS4(76, 77, 78, 79))
+    TMHD_ORS(5, 80, 95, TMHD_RS4(80, 81, 82, 83), TMHD_RS4(84, 85, 86, 87), TMHD_RS4(88, 89, 90, 91),
+             TMHD_RS4(92, 93, 94, 95))
+    TMHD_ORS(6, 96, 111, TMHD_RS4(96, 97, 98, 99), TMHD_RS4(100, 101, 102, 103), TMHD_RS4(104, 105, 106, 107),
+             TMHD_RS4(108, 109, 110, 111))
+    TMHD_ORS(7, 112, 127, TMHD_RS4(112, 113, 114, 115), TMHD_RS4(116, 117, 118, 119),
+             TMHD_RS4(120, 121, 122, 123), TMHD_RS4(124, 125, 126, 127))
+  }
+}
+#undef TMHD_ORS
+#undef TMHD_RS4
+#undef TMHD_RS
+// Wait states after the last MFMA that wrote an AGPR accumulator, before VALU
+// code reads it (an 8-pass MFMA completes within 4 * 8 + 2 cycles).
+__device__ __forceinline__ void mfma_drain() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory"); }
+
+// 16 bytes per lane global -> LDS (saddr form: 64-bit uniform base, 32-bit
+// per-lane offset); the wave's 64 lanes fill the 1 KiB LDS block at m0.
+// Issued as inline asm on purpose: the compiler's wait-count insertion cannot
+// tell the destination block from the tiles being read and would place a
+// vmcnt(0) wait in front of the next LDS read, serialising the prefetch.  The
+// kernel itself waits (vmcnt(0) + barrier) before any read of a loaded tile;
+// extra in-order vector-memory operations unknown to the compiler only make
+// its own vmcnt waits stricter.
+__device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
+}
+
 template <int D, bool I8>
-__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_fwd_kernel(const KArgs a) {
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_fwd_kernel(const KArgs a) {
   constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row in memory
   constexpr int KCPR = KROW / 16;       // 16-byte chunks per key row
   constexpr int KRS = KROW + 16;        // LDS key row stride: one pad chunk, an odd number of chunks
@@ -181,320 +346,394 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   constexpr int NKL = KT / 1024;        // 1 KiB wave loads per key tile
   constexpr int NVL = VT / 1024;
   static_assert(KT % 1024 == 0 && VT % 1024 == 0, "tiles are whole wave loads");
-  constexpr int KWL = (NKL + kWaves - 1) / kWaves;  // per wave (some waves idle if NKL < waves)
+  constexpr int KWL = (NKL + kWaves - 1) / kWaves;  // per wave (the last round is partial)
   constexpr int VWL = (NVL + kWaves - 1) / kWaves;
   constexpr int QST = I8 ? D / 32 : D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;
-  constexpr int NQK = 2 * QST;  // score MFMAs per tile
-  constexpr int NPV = 4 * DB;   // output MFMAs per tile
-  constexpr int LA = 4;         // LDS operand reads in flight ahead of their MFMA
+  constexpr int NQK = QST;     // score slots per 32-key sub-tile (one K operand, two MFMAs)
+  constexpr int NPV = 2 * DB;  // output slots per sub-tile (one V operand, two MFMAs)
+  constexpr int NS = NQK + NPV;
+  constexpr int LA = NQK < 3 ? NQK : 3;  // LDS operand reads in flight ahead of their slot
+  static_assert(LA <= NQK, "the reads prefetched for the next sub-tile are score-slot reads");
 
-  // four distinct LDS objects, so that the compiler can tell the tile being
-  // loaded from the tiles being read (no vmcnt wait in front of the reads)
-  __shared__ __attribute__((aligned(1024))) char kbuf0[KT];
-  __shared__ __attribute__((aligned(1024))) char kbuf1[KT];
-  __shared__ __attribute__((aligned(1024))) char vbuf0[VT];
-  __shared__ __attribute__((aligned(1024))) char vbuf1[VT];
-  auto kbuf = [&](int b) { return b ? kbuf1 : kbuf0; };
-  auto vbuf = [&](int b) { return b ? vbuf1 : vbuf0; };
-
-  // LDS layouts: a 16-lane ds_read_b128 phase reads one 16-byte chunk of 16
-  // consecutive rows; those must fall on 16 distinct 16-byte positions modulo
-  // 256 bytes.  Key and value rows are therefore padded to an odd number of
-  // 16-byte chunks, and every operand read is one base register plus an
-  // immediate offset.
+  // LDS: three K tiles, then three V tiles (tile t lives in buffer t % 3).  A
+  // 16-lane ds_read_b128 phase reads one 16-byte chunk of 16 consecutive rows;
+  // key and value rows are padded to an odd number of 16-byte chunks so those
+  // fall on 16 distinct bank groups and every operand read is one base
+  // register plus an immediate offset.
+  __shared__ __attribute__((aligned(1024))) char smem[3 * KT + 3 * VT];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
 
   const int L = xcd_logical_id(blockIdx.x, gridDim.x);
   const int h = L / a.nqt;
   const int qt = L - h * a.nqt;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
-  const int ql = qt * kBM + w * kQW + lr;  // this lane's query column
+  const int q0 = qt * kBM + w * kQW;                        // first query row of this wave
 
-  // ---- query operand (B operand of S^T = K Q^T), resident for the whole call
-  i32x4 qv[QST];
-  if (ql < a.lq) {
-    if constexpr (I8) {
-      const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
+  // ---- query operands of both 32-row halves (B operands of S^T = K Q^T), pinned in AGPRs
+  i32x4 qv[2][QST];
 #pragma unroll
-      for (int st = 0; st < QST; ++st) qv[st] = *(const i32x4 *)(p + st * 32);
-    } else {
-      const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
-      const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
+  for (int hf = 0; hf < 2; ++hf) {
+    const int ql = q0 + hf * 32 + lr;
+    if (ql < a.lq) {
+      if constexpr (I8) {
+        const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
 #pragma unroll
-      for (int st = 0; st < QST; ++st) {
-        const i32x4 raw = *(const i32x4 *)(p + st * 16);
+        for (int st = 0; st < QST; ++st) qv[hf][st] = *(const i32x4 *)(p + st * 32);
+      } else {
+        const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
+        const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t u = (uint32_t)raw[e];
-          qv[st][e] = (int)pack_bf16x2(__uint_as_float(u << 16) * a.c, __uint_as_float(u & 0xffff0000u) * a.c);
+        for (int st = 0; st < QST; ++st) {
+          const i32x4 raw = *(const i32x4 *)(p + st * 16);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t u = (uint32_t)raw[e];
+            qv[hf][st][e] =
+                (int)pack_bf16x2(__uint_as_float(u << 16) * a.c, __uint_as_float(u & 0xffff0000u) * a.c);
+          }
         }
       }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int st = 0; st < QST; ++st) qv[st] = i32x4{0, 0, 0, 0};
+      for (int st = 0; st < QST; ++st) qv[hf][st] = i32x4{0, 0, 0, 0};
+    }
   }
-  float cq = a.c;  // INT8: softmax scale * log2(e) * query block scale
-  if constexpr (I8) cq = a.c * a.qs[(int64_t)h * a.qshs + (qt * kBM + w * kQW) / TMHD_QUANT_BLOCK];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int st = 0; st < QST; ++st) qpin(hf * QST + st, qv[hf][st]);
+  // INT8: softmax scale * log2(e) * query block scale (the wave's 64 rows lie in one 128-row block)
+  float cq = a.c;
+  if constexpr (I8) cq = a.c * a.qs[(int64_t)h * a.qshs + q0 / TMHD_QUANT_BLOCK];
+  i32x16 magic;  // INT8 score accumulator start
+#pragma unroll
+  for (int r = 0; r < 16; ++r) magic[r] = kI8Magic;
 
-  // per-lane LDS read offsets (bytes; k-step, 32-row half, buffer and db parts are immediates)
+  // per-lane LDS read offsets from smem (bytes; k-step, key half, buffer and db parts are uniform/immediate)
   const uint32_t kro = lr * KRS + g * 16;
-  const uint32_t vro = lr * VRS + g * 16;
+  const uint32_t vro = 3 * KT + lr * VRS + g * 16;
 
   // Tile loads.  LDS slot c (16 bytes) of a tile holds chunk c % (n + 1) of
   // row c / (n + 1) (n data chunks per row; the pad chunk repeats the row's
-  // last chunk).  The per-lane offsets are recomputed at each load from the
-  // lane id (kept opaque so they are not hoisted into registers that would
-  // stay live across the scheduled block).
-  auto slot_row_chunk = [&](int i, int n, int &row, int &chunk) {
-    int l = lane;
-    asm volatile("" : "+v"(l));
-    const int c = (w + i * kWaves) * 64 + l;
-    row = c / (n + 1);
-    chunk = min(c - row * (n + 1), n - 1);
+  // last chunk).  Per-lane source offsets: keys are tile-invariant; values
+  // keep (row, chunk) packed and scale by the segment's row stride per load.
+  uint32_t koff[KWL], vrc[VWL];
+  // Wave w loads blocks w, w + 4, ...; in the last round the waves past the
+  // tile's end repeat its last block (same bytes to the same place), so that
+  // every wave issues the same, branch-free sequence.
+  auto kblk = [&](int i) { return min(w + i * kWaves, NKL - 1); };
+  auto vblk = [&](int i) { return min(w + i * kWaves, NVL - 1); };
+#pragma unroll
+  for (int i = 0; i < KWL; ++i) {
+    const int c = kblk(i) * 64 + lane, row = c / (KCPR + 1), chunk = min(c - row * (KCPR + 1), KCPR - 1);
+    koff[i] = row * KROW + chunk * 16;
+  }
+#pragma unroll
+  for (int i = 0; i < VWL; ++i) {
+    const int c = vblk(i) * 64 + lane, row = c / 9, chunk = min(c - row * 9, 7);
+    vrc[i] = (uint32_t)row | ((uint32_t)chunk << 20);
+  }
+  // load n of a tile: K blocks first (n < KWL), then V blocks
+  constexpr int NLD = KWL + VWL;
+  auto load_one = [&](int n, const char *kbase, uint32_t kdst, const char *vbase, uint32_t vrs2, uint32_t vdst) {
+    if (n < KWL)
+      load_lds16(kbase, koff[n], kdst + kblk(n) * 1024);
+    else
+      load_lds16(vbase, (vrc[n - KWL] & 0xfffffu) * vrs2 + ((vrc[n - KWL] >> 20) << 4), vdst + vblk(n - KWL) * 1024);
   };
-  auto load_k = [&](const Stream &S, char *dst) {
+  auto load_k = [&](const Stream &S, int buf) {
     const char *base = S.kb + (int64_t)S.t * (kBN * KROW);
 #pragma unroll
-    for (int i = 0; i < KWL; ++i)
-      if (NKL % kWaves == 0 || w + i * kWaves < NKL) {
-        int row, chunk;
-        slot_row_chunk(i, KCPR, row, chunk);
-        load_lds16(base + (uint32_t)(row * KROW + chunk * 16), dst + (w + i * kWaves) * 1024);
-      }
+    for (int i = 0; i < KWL; ++i) load_lds16(base, koff[i], lds0 + buf * KT + kblk(i) * 1024);
   };
-  auto load_v = [&](const Stream &S, char *dst) {
+  auto load_v = [&](const Stream &S, int buf) {
     const char *base = S.vb + S.t * (kBN * 2);
 #pragma unroll
     for (int i = 0; i < VWL; ++i)
-      if (NVL % kWaves == 0 || w + i * kWaves < NVL) {
-        int row, chunk;
-        slot_row_chunk(i, 8, row, chunk);
-        load_lds16(base + ((uint32_t)row * S.vrs2 + (uint32_t)chunk * 16), dst + (w + i * kWaves) * 1024);
-      }
+      load_lds16(base, (vrc[i] & 0xfffffu) * S.vrs2 + ((vrc[i] >> 20) << 4),
+                 lds0 + 3 * KT + buf * VT + vblk(i) * 1024);
   };
   // INT8 key scale of a tile, read through the vector memory path (counted by
-  // vmcnt, so the end-of-iteration wait covers it instead of an lgkmcnt wait
-  // inside the scheduled block)
+  // vmcnt, so the end-of-iteration wait covers it)
   auto load_ks = [&](const Stream &S) {
     int idx = S.t >> 1;  // 128-token quant blocks hold two tiles
     asm volatile("v_mov_b32 %0, %1" : "=v"(idx) : "s"(idx));
     return S.ks[idx];
   };
+  auto lds_read = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
+  // valid keys of a stream's current tile (1 .. 64)
+  auto tile_valid = [](const Stream &S) { return min(S.tok - S.t * kBN, kBN); };
 
-  // S^T = K Q^T for the 64 keys of a tile: lane holds keys 32kb + 8(r/4) + 4g + r%4
-  auto qk = [&](const char *kb, const f32x16 &init, const i32x16 &init8, f32x16 (&sc)[2], float ct, float nb) {
-    if constexpr (I8) {
-      i32x16 ia[2] = {init8, init8};
+  // keys of a 32-key sub-tile at or beyond nvalid (relative to the sub-tile) -> -inf
+  auto mask_sub = [&](f32x16 (&s)[2], int nvalid) {
 #pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-        for (int st = 0; st < QST; ++st)
-          ia[kb32] = mfma_i8(*(const i32x4 *)(kb + kb32 * 32 * KRS + st * 32 + kro), qv[st], ia[kb32]);
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sc[kb32][r] = fmaf(__int_as_float(ia[kb32][r]), ct, nb);
-    } else {
-#pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) {
-        sc[kb32] = init;
-#pragma unroll
-        for (int st = 0; st < QST; ++st)
-          sc[kb32] = mfma_bf16(*(const i32x4 *)(kb + kb32 * 32 * KRS + st * 32 + kro), qv[st], sc[kb32]);
-      }
-    }
-  };
-  auto mask_tail = [&](f32x16 (&sc)[2], int nvalid) {
-#pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32)
+    for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (kb32 * 32 + 8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) sc[kb32][r] = -INFINITY;
+        if (8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) s[hf][r] = -INFINITY;
   };
-  auto lane_max = [](const f32x16 (&sc)[2]) {
-    float m = fmaxf(sc[0][0], sc[0][1]);
+  auto sub_max = [](const f32x16 &s) {
+    float m = fmaxf(s[0], s[1]);
 #pragma unroll
-    for (int r = 2; r < 16; r += 2) m = fmaxf(m, fmaxf(sc[0][r], sc[0][r + 1]));
-#pragma unroll
-    for (int r = 0; r < 16; r += 2) m = fmaxf(m, fmaxf(sc[1][r], sc[1][r + 1]));
+    for (int r = 2; r < 16; r += 2) m = fmaxf(m, fmaxf(s[r], s[r + 1]));
     return m;
   };
 
-  f32x16 o[DB];
+  f32x16 o[2][DB];  // block hf * DB + db lives in AGPRs a[16 b, 16 b + 15]
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
-  float lsum = 0.0f;
-  f32x16 negm;  // BF16: -m in every element (the score accumulator's start value)
-  i32x16 magic;
+    for (int db = 0; db < DB; ++db) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    negm[r] = 0.0f;
-    magic[r] = kI8Magic;
-  }
+      for (int r = 0; r < 16; ++r) o[hf][db][r] = 0.0f;
+      opin(hf * DB + db, o[hf][db]);
+    }
+  float lsum[2] = {0.0f, 0.0f};
+  float mref[2];   // running reference of each query half (log2 units)
+  f32x16 negm[2];  // BF16: -mref in every element, the score accumulator start
+  const f32x16 zero16 = {};
 
-  // ---- prologue: K(0), V(0), K(1) resident; S = scores of tile 0
-  Stream s0;
-  stream_set<I8>(s0, a, h, 0);
-  Stream sv = s0;  // V stream: tile j + 1 during iteration j
-  stream_next<I8>(sv, a, h);
-  Stream sk = sv;  // K stream: tile j + 2 during iteration j
-  stream_next<I8>(sk, a, h);
-  load_k(s0, kbuf(0));
-  load_v(s0, vbuf(0));
-  load_k(sv, kbuf(1));
-  float ks_n = 0.0f, ks0 = 0.0f;  // INT8: key scale of tile j + 1
+  // ---- prologue: K(0..2), V(0..1) resident; S = scores of sub-tile 0 (minus m)
+  Stream t0, t1, t2, t3;
+  stream_set<I8>(t0, a, h, 0);
+  t1 = t0;
+  stream_next<I8>(t1, a, h);
+  t2 = t1;
+  stream_next<I8>(t2, a, h);
+  t3 = t2;
+  stream_next<I8>(t3, a, h);
+  load_k(t0, 0);
+  load_k(t1, 1);
+  load_v(t0, 0);
+  // valid keys and INT8 key scales of tiles j, j+1, j+2, j+3
+  int nv0 = tile_valid(t0), nv1 = tile_valid(t1), nv2 = tile_valid(t2), nv3 = tile_valid(t3);
+  float ks0 = 0.0f, ks1 = 0.0f, ks2 = 0.0f;
   if constexpr (I8) {
-    ks0 = load_ks(s0);
-    ks_n = load_ks(sv);
+    ks0 = load_ks(t0);
+    ks1 = load_ks(t1);
+    ks2 = load_ks(t2);
   }
   wait_vmem();
   __syncthreads();
-  f32x16 sc[2];
-  float mref;
+  f32x16 sc[2];  // scores of the current sub-tile (minus m)
   {
     const float ct0 = cq * ks0;
-    qk(kbuf(0), negm, magic, sc, ct0, -kI8MagicF * ct0);
-    if (s0.tok < kBN) mask_tail(sc, s0.tok);
-    const float lm = lane_max(sc);
-    mref = fmaxf(lm, __shfl_xor(lm, 32));
+    if constexpr (I8) {
+      i32x16 acc[2];
 #pragma unroll
-    for (int kb32 = 0; kb32 < 2; ++kb32) sc[kb32] -= mref;
-    negm = -mref;
+      for (int st = 0; st < QST; ++st) {
+        const i32x4 kv = lds_read(kro + st * 32);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) qk_i8(hf * QST + st, st == 0, acc[hf], kv, qv[hf][st], magic);
+      }
+      mfma_drain();
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sc[hf][r] = fmaf(__int_as_float(acc[hf][r]), ct0, -kI8MagicF * ct0);
+    } else {
+#pragma unroll
+      for (int st = 0; st < QST; ++st) {
+        const i32x4 kv = lds_read(kro + st * 32);
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) qk_bf16(hf * QST + st, st == 0, sc[hf], kv, qv[hf][st], zero16);
+      }
+      mfma_drain();
+    }
+    if (nv0 < 32) mask_sub(sc, nv0);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const float lm = sub_max(sc[hf]);
+      mref[hf] = fmaxf(lm, __shfl_xor(lm, 32));
+      sc[hf] -= mref[hf];
+      negm[hf] = -mref[hf];
+    }
   }
-  __syncthreads();  // every wave is done with K(0) before K(2) overwrites it
+  // load streams: K of tile j+3 and V of tile j+2, issued after the barrier of iteration j
+  Stream sk = t3, sv = t2;
+  // operands of the first slots of sub-tile (0, keys 32..63)
+  i32x4 pre[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) pre[i] = lds_read(kro + 32 * KRS + i * 32);
 
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
-  int j = 0;
-  // iteration 0 loads K(2) and V(1)
-  load_k(sk, kbuf(0));
-  load_v(sv, vbuf(1));
-  float ks_nn = 0.0f;  // INT8: key scale of tile j + 2
-  if constexpr (I8) ks_nn = load_ks(sk);
-  // One tile; B = j & 1 selects the buffers statically.  Returns false after the last tile.
-  auto iter = [&](auto par) -> bool {
-    constexpr int B = decltype(par)::value;
-    const float ct_n = cq * ks_n;
-    const float nb_n = -fmaf(kI8MagicF, ct_n, mref);
+  int j = 0, b0 = 0, b1 = 1, b2 = 2;  // LDS buffers of tiles j, j+1, j+2
 
-    // The block below is software-pipelined by hand in NS slots, fenced so
-    // that the compiler keeps the order: slot i issues the LDS operand read of
-    // MFMA i + LA, runs MFMA i and a fixed share of the VALU work.
-    //   slots [0, NQK):  S(j+1) = K Q^T (key half kb32 = i / QST, k-step st),
-    //                    under P(j) = exp2(S(j)) -> bf16 pairs and row sums;
-    //   slots [NQK, NS): O^T += V^T P^T (kb32, st, db), under the row maxima
-    //                    of S(j+1) (INT8: after its dequantisation).
-    // After the last tile the score MFMAs read a stale in-bounds buffer and
-    // their result is unused.
-    constexpr int NS = NQK + NPV;
-    constexpr int PPS = 16 / NQK;  // P pairs per score slot
-    constexpr int MPS = 16 / NPV;  // max pairs per output slot
+  // One 32-key sub-tile, software-pipelined by hand in NS slots fenced so
+  // that the compiler keeps their order.  Slot i issues the LDS operand read
+  // of slot i + LA, its VALU share, then its two MFMAs (one per query half):
+  //   slots [0, NQK):  scores of the next sub-tile, K rows at kb (k-step st = i),
+  //                    under P = exp2(S) of the current sub-tile -> bf16 pairs, row sums;
+  //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile, V chunks at vb,
+  //                    under the scaling (INT8) / shift (BF16) and row maxima of
+  //                    the next sub-tile's scores.
+  // nvs: valid keys of the next sub-tile (<= 0: none); ctn: INT8 dequantisation
+  // of its scores; live: the next sub-tile exists.  Leaves the next sub-tile's
+  // scores (minus m) in sc.
+  // With loads, the slots also issue the tile loads of the iteration (load n
+  // in slot n + 1).  pre: the operands of the first LA slots, read by the
+  // previous sub-tile; on return, those of the next sub-tile (K rows at kbn).
+  auto sub_tile = [&](uint32_t kb, uint32_t vb, uint32_t kbn, i32x4 (&pre)[LA], int nvs, float ctn, bool live,
+                      bool loads, const char *lkb, uint32_t lkd, const char *lvb, uint32_t lvrs, uint32_t lvd) {
+    const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
     auto read_op = [&](int i) -> i32x4 {
-      if (i < NQK) {
-        const int kb32 = i / QST, st = i % QST;
-        return *(const i32x4 *)(kbuf(B ^ 1) + kb32 * 32 * KRS + st * 32 + kro);
-      }
-      const int pv = i - NQK, kb32 = pv / (2 * DB), st = (pv / DB) & 1, db = pv % DB;
-      return *(const i32x4 *)(vbuf(B) + db * 32 * VRS + (4 * kb32 + 2 * st) * 16 + vro);
+      if (i < NQK) return lds_read(kb + i * 32);
+      const int p = i - NQK, st = p / DB, db = p % DB;
+      return lds_read(vb + db * 32 * VRS + 2 * st * 16);
     };
     i32x4 ops[NS];
-    i32x4 pkv[2][2];  // P(j) as bf16 pairs: [kb32][st] = keys 16 st .. of the half, 4 dwords
-    float ts = 0.0f;
+    i32x4 pk[2][2];  // P as bf16 pairs: [query half][16-key step]
     f32x16 sn[2];
     i32x16 sni[2];
-    float lm = -INFINITY;
+    float ts[2] = {0.0f, 0.0f};
+    float lm[2] = {-INFINITY, -INFINITY};
 #pragma unroll
-    for (int i = 0; i < LA; ++i) ops[i] = read_op(i);
-#pragma unroll
+    for (int i = 0; i < LA; ++i) ops[i] = pre[i];
+#pragma clang loop unroll(full)
     for (int i = 0; i < NS; ++i) {
-      if (i + LA < NS) ops[i + LA] = read_op(i + LA);
+      if (i + LA < NS)
+        ops[i + LA] = read_op(i + LA);
+      else
+        pre[i + LA - NS] = lds_read(kbn + (i + LA - NS) * 32);
+      if (loads && i >= 1 && i - 1 < NLD) load_one(i - 1, lkb, lkd, lvb, lvrs, lvd);
       if (i < NQK) {
-        const int kb32 = i / QST, st = i % QST;
-        if constexpr (I8) {
-          sni[kb32] = mfma_i8(ops[i], qv[st], st == 0 ? magic : sni[kb32]);
-        } else {
-          sn[kb32] = mfma_bf16(ops[i], qv[st], st == 0 ? negm : sn[kb32]);
-        }
+        // P pairs q of both query halves whose slot is i
 #pragma unroll
-        for (int u = 0; u < PPS; ++u) {
-          const int q = i * PPS + u, pk32 = q >> 3, r = (q & 7) * 2;
-          const uint32_t pr =
-              pack_bf16x2(__builtin_amdgcn_exp2f(sc[pk32][r]), __builtin_amdgcn_exp2f(sc[pk32][r + 1]));
-          pkv[pk32][(q >> 2) & 1][q & 3] = (int)pr;
-          ts = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pr), ones, ts, false);
+        for (int q = 0; q < 8; ++q)
+          if (q * NQK / 8 == i)
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf) {
+              const uint32_t pr =
+                  pack_bf16x2(__builtin_amdgcn_exp2f(sc[hf][2 * q]), __builtin_amdgcn_exp2f(sc[hf][2 * q + 1]));
+              pk[hf][q >> 2][q & 3] = (int)pr;
+              ts[hf] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pr), ones, ts[hf], false);
+              asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this slot
+            }
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          if constexpr (I8)
+            qk_i8(hf * QST + i, i == 0, sni[hf], ops[i], qv[hf][i], magic);
+          else
+            qk_bf16(hf * QST + i, i == 0, sn[hf], ops[i], qv[hf][i], negm[hf]);
         }
       } else {
-        const int pv = i - NQK, kb32 = pv / (2 * DB), st = (pv / DB) & 1, db = pv % DB;
-        o[db] = mfma_bf16(ops[i], pkv[kb32][st], o[db]);
+        const int p = i - NQK, st = p / DB, db = p % DB;
+        // the next sub-tile's scores: first read one output slot after the
+        // last score MFMA, behind 16 wait states
+        if (p == 1) asm volatile("s_nop 15" ::: "memory");
+        if (p >= 1)
 #pragma unroll
-        for (int u = 0; u < MPS; ++u) {
-          const int q = pv * MPS + u, m32 = q >> 3, r = (q & 7) * 2;
-          if constexpr (I8) {
-            sn[m32][r] = fmaf(__int_as_float(sni[m32][r]), ct_n, nb_n);
-            sn[m32][r + 1] = fmaf(__int_as_float(sni[m32][r + 1]), ct_n, nb_n);
-          }
-          lm = fmaxf(lm, fmaxf(sn[m32][r], sn[m32][r + 1]));
-        }
+          for (int q = 0; q < 16; ++q)  // [query half][pair]
+            if (q * (NPV - 1) / 16 == p - 1) {
+              const int hf = q >> 3, r = (q & 7) * 2;
+              if constexpr (I8) {
+                sn[hf][r] = fmaf(__int_as_float(sni[hf][r]), ctn, nbn[hf]);
+                sn[hf][r + 1] = fmaf(__int_as_float(sni[hf][r + 1]), ctn, nbn[hf]);
+              }
+              lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][r], sn[hf][r + 1]));
+              asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this slot
+            }
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) pv(hf * DB + db, db == 0, o[hf][db], ops[i], pk[hf][st]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    lsum += ts;
-
-    if (++j >= a.ntiles) return false;
-    // tile j (the new current tile) is the last, partial tile of its segment
-    const int nv = sv.tok - sv.t * kBN;
-    if (nv < kBN) {
-      asm volatile("" ::: "memory");
-      mask_tail(sn, nv);
-      lm = lane_max(sn);
+    lsum[0] += ts[0];
+    lsum[1] += ts[1];
+    if (!live) return;
+    if (nvs < 32) {
+      int nvo = nvs;  // opaque inside the branch: keeps the comparisons from being hoisted
+      asm volatile("" : "+s"(nvo));
+      mask_sub(sn, nvo);
+      lm[0] = sub_max(sn[0]);
+      lm[1] = sub_max(sn[1]);
     }
-    if (__any(lm > kLazyRescale)) {
-      const float cm = fmaxf(lm, __shfl_xor(lm, 32));
-      const float delta = fmaxf(cm, 0.0f);
-      const float alpha = __builtin_amdgcn_exp2f(-delta);
-      lsum *= alpha;
+    if (__any(fmaxf(lm[0], lm[1]) > kLazyRescale)) {
+      mfma_drain();
 #pragma unroll
-      for (int db = 0; db < DB; ++db) o[db] *= alpha;
+      for (int hf = 0; hf < 2; ++hf) {
+        const float cm = fmaxf(lm[hf], __shfl_xor(lm[hf], 32));
+        const float delta = fmaxf(cm, 0.0f);
+        const float alpha = __builtin_amdgcn_exp2f(-delta);
+        lsum[hf] *= alpha;
 #pragma unroll
-      for (int kb32 = 0; kb32 < 2; ++kb32) sn[kb32] -= delta;
-      mref += delta;
-      negm = -mref;
+        for (int db = 0; db < DB; ++db) orescale(hf * DB + db, o[hf][db], alpha);
+        sn[hf] -= delta;
+        mref[hf] += delta;
+        negm[hf] = -mref[hf];
+      }
+      asm volatile("s_nop 2" ::: "memory");
     }
     sc[0] = sn[0];
     sc[1] = sn[1];
-    ks_n = ks_nn;
+  };
+
+  // Iteration j: sub-tiles (j, keys 0..31) and (j, keys 32..63).  LDS holds
+  // K(j), K(j+1) and V(j); the loads issued from its first sub-tile's slots
+  // (K(j+2) over K(j-1), V(j+1) over V(j-2)) are waited for at its end.
+  // tile loads issued from the slots of iteration j: K(j+2) and V(j+1)
+  const char *lkb = t2.kb + (int64_t)t2.t * (kBN * KROW), *lvb = t1.vb + t1.t * (kBN * 2);
+  uint32_t lvrs = t1.vrs2, lkd = lds0 + 2 * KT, lvd = lds0 + 3 * KT + 1 * VT;
+  for (;;) {
+    // P of keys 0..31 of tile j; scores of keys 32..63 of tile j come next
+    sub_tile(kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, true, lkb, lkd, lvb,
+             lvrs, lvd);
+    // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 come next
+    // (after the last tile they read a stale in-bounds buffer and are unused)
+    const bool more = j + 1 < a.ntiles;
+    sub_tile(kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, false, lkb,
+             lkd, lvb, lvrs, lvd);
+    if (!more) break;
+    ++j;
+    wait_vmem();     // this wave's loads of K(j+1), V(j) (tile numbers of the new j)
+    __syncthreads();  // everyone's loads landed; K(j-1) and V(j-2) are free
+    nv0 = nv1;
+    nv1 = nv2;
+    nv2 = nv3;
+    ks0 = ks1;
+    ks1 = ks2;
+    const int bf = b0;  // buffers rotate: tile t lives in buffer t % 3
+    b0 = b1;
+    b1 = b2;
+    b2 = bf;
+    // K(j+2) over K(j-1) and V(j+1) over V(j-2), issued from the slots of the
+    // first sub-tile of iteration j
+    lkb = sk.kb + (int64_t)sk.t * (kBN * KROW);
+    lkd = lds0 + b2 * KT;
+    lvb = sv.vb + sv.t * (kBN * 2);
+    lvrs = sv.vrs2;
+    lvd = lds0 + 3 * KT + b1 * VT;
+    if constexpr (I8) ks2 = load_ks(sk);
     sv = sk;
     stream_next<I8>(sk, a, h);
-    wait_vmem();
-    __syncthreads();
-    // K(j+3) into the buffer K(j+1) used, V(j+2) into the buffer V(j) used
-    load_k(sk, kbuf(B ^ 1));
-    load_v(sv, vbuf(B));
-    if constexpr (I8) ks_nn = load_ks(sk);
-    return true;
-  };
-  for (;;) {
-    if (!iter(std::integral_constant<int, 0>{})) break;
-    if (!iter(std::integral_constant<int, 1>{})) break;
+    nv3 = tile_valid(sk);
   }
 
   // ---- epilogue: O = O^T / l, written token-major (4 consecutive d per store)
-  const float lt = lsum + __shfl_xor(lsum, 32);
-  const float inv = 1.0f / lt;
-  if (ql < a.lq) {
-    const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
-    uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
+  mfma_drain();
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+  for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        i32x2 pr = {(int)pack_bf16x2(o[db][4 * u] * inv, o[db][4 * u + 1] * inv),
-                    (int)pack_bf16x2(o[db][4 * u + 2] * inv, o[db][4 * u + 3] * inv)};
-        *(i32x2 *)(op + db * 32 + 8 * u) = pr;
-      }
+    for (int db = 0; db < DB; ++db) opin(hf * DB + db, o[hf][db]);
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
+    const float inv = 1.0f / lt;
+    const int ql = q0 + hf * 32 + lr;
+    if (ql < a.lq) {
+      const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
+      uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          i32x2 pr = {(int)pack_bf16x2(o[hf][db][4 * u] * inv, o[hf][db][4 * u + 1] * inv),
+                      (int)pack_bf16x2(o[hf][db][4 * u + 2] * inv, o[hf][db][4 * u + 3] * inv)};
+          *(i32x2 *)(op + db * 32 + 8 * u) = pr;
+        }
+    }
   }
 }
 
