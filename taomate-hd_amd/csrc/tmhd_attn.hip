@@ -36,12 +36,15 @@
 //
 // Pipeline: a tile is two 32-key sub-tiles; each sub-tile is one basic block
 // of fenced slots, each slot one LDS operand read (issued three slots ahead)
-// and two MFMAs (one per query half) plus its share of VALU work:
-//   exp2 / pack / row-sum of P(s)      under the score MFMAs of sub-tile s+1,
-//   scaling and row max of S(s+1)      under the P.V MFMAs of sub-tile s,
+// and two MFMAs (one per query half) plus its share of the other work, spread
+// by a compile-time plan that evens out the instructions per slot:
+//   exp2 / pack / row-sum of P(s)      under the score MFMAs of sub-tile s+1
+//                                      and the first P.V MFMAs of sub-tile s,
+//   scaling and row max of S(s+1)      under the later P.V MFMAs of sub-tile s,
 //   the tile loads of the iteration    in the first sub-tile's slots.
 // The last slots read the first operands of the next sub-tile.  Rare work
 // (partial tiles, rescale, segment switches) sits in branches after the block.
+// Scores of consecutive sub-tiles alternate between two register sets.
 #include <math.h>
 
 #include <type_traits>
@@ -154,8 +157,9 @@ __device__ __forceinline__ void stream_next(Stream &S, const KArgs &a, int h) {
 //   * VALU write -> MFMA operand read needs 2 wait states: the first MFMA that
 //     reads a freshly packed P group uses the *_fresh form (s_nop 1);
 //   * MFMA result -> VALU read (12 wait states for either MFMA): score results
-//     are first read one slot (two MFMAs) plus 16 wait states after the last
-//     score MFMA; AGPR accumulators are read only after mfma_drain();
+//     are first read behind an s_nop 9 in the second output slot, which names
+//     them so that no read moves above it; AGPR accumulators are read only
+//     after mfma_drain();
 //   * accvgpr write (rescale) -> MFMA accumulate: s_nop 2 after the rescale;
 //   * the rescale itself reads each AGPR after mfma_drain();
 //   * back-to-back accumulation into the same registers needs no wait states.
@@ -335,6 +339,40 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
+// Work plan of one sub-tile's slots, fixed at compile time.  Units:
+//   P(u): exp2 / bf16 pack / row sum of pair u % 8 (keys 2q, 2q+1) of query
+//         half u / 8 of the current sub-tile; pairs 0..3 feed the first P.V
+//         k-step (slot nqk), pairs 4..7 the second (slot nqk + db);
+//   M(u): INT8 dequantisation and row maximum of pair u % 8, half u / 8 of
+//         the next sub-tile's scores, after its score chain (slot nqk + 1 on);
+//   L(n): tile load n, in the first `lwin` slots.
+// Each slot starts at the cost of its operand read and wait; every unit goes
+// to the cheapest slot of its window (the earliest on ties).
+struct SlotPlan {
+  int p[16], m[16], l[16];
+};
+constexpr int plan_put(int (&cost)[32], int lo, int hi, int c) {
+  int best = lo;
+  for (int i = lo + 1; i <= hi; ++i)
+    if (cost[i] < cost[best]) best = i;
+  cost[best] += c;
+  return best;
+}
+constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i8) {
+  SlotPlan s{};
+  int cost[32] = {};
+  const int ns = nqk + npv;
+  for (int i = 0; i < ns; ++i) cost[i] = 2;
+  for (int q = 0; q < 4; ++q)
+    for (int hf = 0; hf < 2; ++hf) s.p[hf * 8 + q] = plan_put(cost, 0, nqk - 1, 6);
+  for (int q = 0; q < 8; ++q)
+    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, nqk + 1, ns - 1, i8 ? 3 : 1);
+  for (int q = 4; q < 8; ++q)
+    for (int hf = 0; hf < 2; ++hf) s.p[hf * 8 + q] = plan_put(cost, 0, nqk + db - 1, 6);
+  for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 3) : -1;
+  return s;
+}
+
 template <int D, bool I8>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_fwd_kernel(const KArgs a) {
   constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row in memory
@@ -355,6 +393,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   constexpr int NS = NQK + NPV;
   constexpr int LA = NQK < 3 ? NQK : 3;  // LDS operand reads in flight ahead of their slot
   static_assert(LA <= NQK, "the reads prefetched for the next sub-tile are score-slot reads");
+  static_assert(NS <= 32 && NPV >= 2, "slot plan bounds");
 
   // LDS: three K tiles, then three V tiles (tile t lives in buffer t % 3).  A
   // 16-lane ds_read_b128 phase reads one 16-byte chunk of 16 consecutive rows;
@@ -437,11 +476,20 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   }
   // load n of a tile: K blocks first (n < KWL), then V blocks
   constexpr int NLD = KWL + VWL;
-  auto load_one = [&](int n, const char *kbase, uint32_t kdst, const char *vbase, uint32_t vrs2, uint32_t vdst) {
+  static_assert(NLD <= 16, "slot plan bounds");
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, 3 * NS / 4, I8);  // sub-tiles with tile loads
+  constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8);               // sub-tiles without
+  // value source offsets for the V^T row stride of the current load segment
+  uint32_t voff[VWL];
+  auto set_voff = [&](uint32_t vrs2) {
+#pragma unroll
+    for (int i = 0; i < VWL; ++i) voff[i] = (vrc[i] & 0xfffffu) * vrs2 + ((vrc[i] >> 20) << 4);
+  };
+  auto load_one = [&](int n, const char *kbase, uint32_t kdst, const char *vbase, uint32_t vdst) {
     if (n < KWL)
       load_lds16(kbase, koff[n], kdst + kblk(n) * 1024);
     else
-      load_lds16(vbase, (vrc[n - KWL] & 0xfffffu) * vrs2 + ((vrc[n - KWL] >> 20) << 4), vdst + vblk(n - KWL) * 1024);
+      load_lds16(vbase, voff[n - KWL], vdst + vblk(n - KWL) * 1024);
   };
   auto load_k = [&](const Stream &S, int buf) {
     const char *base = S.kb + (int64_t)S.t * (kBN * KROW);
@@ -517,7 +565,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   }
   wait_vmem();
   __syncthreads();
-  f32x16 sc[2];  // scores of the current sub-tile (minus m)
+  // scores (minus m) of the current and the next sub-tile: sub-tiles alternate
+  // between the two sets, so no copies are needed
+  f32x16 sA[2], sB[2];
   {
     const float ct0 = cq * ks0;
     if constexpr (I8) {
@@ -532,22 +582,22 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sc[hf][r] = fmaf(__int_as_float(acc[hf][r]), ct0, -kI8MagicF * ct0);
+        for (int r = 0; r < 16; ++r) sA[hf][r] = fmaf(__int_as_float(acc[hf][r]), ct0, -kI8MagicF * ct0);
     } else {
 #pragma unroll
       for (int st = 0; st < QST; ++st) {
         const i32x4 kv = lds_read(kro + st * 32);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) qk_bf16(hf * QST + st, st == 0, sc[hf], kv, qv[hf][st], zero16);
+        for (int hf = 0; hf < 2; ++hf) qk_bf16(hf * QST + st, st == 0, sA[hf], kv, qv[hf][st], zero16);
       }
       mfma_drain();
     }
-    if (nv0 < 32) mask_sub(sc, nv0);
+    if (nv0 < 32) mask_sub(sA, nv0);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
-      const float lm = sub_max(sc[hf]);
+      const float lm = sub_max(sA[hf]);
       mref[hf] = fmaxf(lm, __shfl_xor(lm, 32));
-      sc[hf] -= mref[hf];
+      sA[hf] -= mref[hf];
       negm[hf] = -mref[hf];
     }
   }
@@ -558,25 +608,23 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
   for (int i = 0; i < LA; ++i) pre[i] = lds_read(kro + 32 * KRS + i * 32);
 
-  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
   int j = 0, b0 = 0, b1 = 1, b2 = 2;  // LDS buffers of tiles j, j+1, j+2
 
   // One 32-key sub-tile, software-pipelined by hand in NS slots fenced so
   // that the compiler keeps their order.  Slot i issues the LDS operand read
-  // of slot i + LA, its VALU share, then its two MFMAs (one per query half):
-  //   slots [0, NQK):  scores of the next sub-tile, K rows at kb (k-step st = i),
-  //                    under P = exp2(S) of the current sub-tile -> bf16 pairs, row sums;
-  //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile, V chunks at vb,
-  //                    under the scaling (INT8) / shift (BF16) and row maxima of
-  //                    the next sub-tile's scores.
-  // nvs: valid keys of the next sub-tile (<= 0: none); ctn: INT8 dequantisation
-  // of its scores; live: the next sub-tile exists.  Leaves the next sub-tile's
-  // scores (minus m) in sc.
-  // With loads, the slots also issue the tile loads of the iteration (load n
-  // in slot n + 1).  pre: the operands of the first LA slots, read by the
-  // previous sub-tile; on return, those of the next sub-tile (K rows at kbn).
-  auto sub_tile = [&](uint32_t kb, uint32_t vb, uint32_t kbn, i32x4 (&pre)[LA], int nvs, float ctn, bool live,
-                      bool loads, const char *lkb, uint32_t lkd, const char *lvb, uint32_t lvrs, uint32_t lvd) {
+  // of slot i + LA, the units the slot plan gives it, then its two MFMAs (one
+  // per query half):
+  //   slots [0, NQK):  scores of the next sub-tile, K rows at kb (k-step st = i);
+  //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile, V chunks at vb.
+  // sc: scores (minus m) of the current sub-tile; sn: receives those of the
+  // next.  nvs: valid keys of the next sub-tile (<= 0: none); ctn: INT8
+  // dequantisation of its scores; live: the next sub-tile exists.
+  // With loads, the slots also issue the tile loads of the iteration.  pre:
+  // the operands of the first LA slots, read by the previous sub-tile; on
+  // return, those of the next sub-tile (K rows at kbn).
+  auto sub_tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], uint32_t kb, uint32_t vb, uint32_t kbn, i32x4 (&pre)[LA],
+                      int nvs, float ctn, bool live, bool loads, const char *lkb, uint32_t lkd, const char *lvb,
+                      uint32_t lvd) {
     const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
     auto read_op = [&](int i) -> i32x4 {
       if (i < NQK) return lds_read(kb + i * 32);
@@ -585,7 +633,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     };
     i32x4 ops[NS];
     i32x4 pk[2][2];  // P as bf16 pairs: [query half][16-key step]
-    f32x16 sn[2];
     i32x16 sni[2];
     float ts[2] = {0.0f, 0.0f};
     float lm[2] = {-INFINITY, -INFINITY};
@@ -593,24 +640,46 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     for (int i = 0; i < LA; ++i) ops[i] = pre[i];
 #pragma clang loop unroll(full)
     for (int i = 0; i < NS; ++i) {
+      const SlotPlan &pl = loads ? PL : PN;
       if (i + LA < NS)
         ops[i + LA] = read_op(i + LA);
       else
         pre[i + LA - NS] = lds_read(kbn + (i + LA - NS) * 32);
-      if (loads && i >= 1 && i - 1 < NLD) load_one(i - 1, lkb, lkd, lvb, lvrs, lvd);
+      if (loads)
+#pragma unroll
+        for (int n = 0; n < NLD; ++n)
+          if (pl.l[n] == i) load_one(n, lkb, lkd, lvb, lvd);
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.p[u] == i) {
+          const int hf = u >> 3, q = u & 7;
+          const float e0 = __builtin_amdgcn_exp2f(sc[hf][2 * q]), e1 = __builtin_amdgcn_exp2f(sc[hf][2 * q + 1]);
+          pk[hf][q >> 2][q & 3] = (int)pack_bf16x2(e0, e1);
+          ts[hf] += e0;
+          ts[hf] += e1;
+          asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this slot
+        }
+      if (i == NQK + 1) {
+        // first reads of the next sub-tile's scores: at least 12 wait states
+        // after the last score MFMA (slot NQK's two MFMAs, its operand read and
+        // wait, and these 10); naming the results keeps every read below
+        if constexpr (I8)
+          asm volatile("s_nop 9" : "+v"(sni[0]), "+v"(sni[1]));
+        else
+          asm volatile("s_nop 9" : "+v"(sn[0]), "+v"(sn[1]));
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.m[u] == i) {
+          const int hf = u >> 3, r = (u & 7) * 2;
+          if constexpr (I8) {
+            sn[hf][r] = fmaf(__int_as_float(sni[hf][r]), ctn, nbn[hf]);
+            sn[hf][r + 1] = fmaf(__int_as_float(sni[hf][r + 1]), ctn, nbn[hf]);
+          }
+          lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][r], sn[hf][r + 1]));
+          asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this slot
+        }
       if (i < NQK) {
-        // P pairs q of both query halves whose slot is i
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (q * NQK / 8 == i)
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf) {
-              const uint32_t pr =
-                  pack_bf16x2(__builtin_amdgcn_exp2f(sc[hf][2 * q]), __builtin_amdgcn_exp2f(sc[hf][2 * q + 1]));
-              pk[hf][q >> 2][q & 3] = (int)pr;
-              ts[hf] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pr), ones, ts[hf], false);
-              asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this slot
-            }
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) {
           if constexpr (I8)
@@ -620,21 +689,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         }
       } else {
         const int p = i - NQK, st = p / DB, db = p % DB;
-        // the next sub-tile's scores: first read one output slot after the
-        // last score MFMA, behind 16 wait states
-        if (p == 1) asm volatile("s_nop 15" ::: "memory");
-        if (p >= 1)
-#pragma unroll
-          for (int q = 0; q < 16; ++q)  // [query half][pair]
-            if (q * (NPV - 1) / 16 == p - 1) {
-              const int hf = q >> 3, r = (q & 7) * 2;
-              if constexpr (I8) {
-                sn[hf][r] = fmaf(__int_as_float(sni[hf][r]), ctn, nbn[hf]);
-                sn[hf][r + 1] = fmaf(__int_as_float(sni[hf][r + 1]), ctn, nbn[hf]);
-              }
-              lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][r], sn[hf][r + 1]));
-              asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this slot
-            }
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf) pv(hf * DB + db, db == 0, o[hf][db], ops[i], pk[hf][st]);
       }
@@ -666,8 +720,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       }
       asm volatile("s_nop 2" ::: "memory");
     }
-    sc[0] = sn[0];
-    sc[1] = sn[1];
   };
 
   // Iteration j: sub-tiles (j, keys 0..31) and (j, keys 32..63).  LDS holds
@@ -676,15 +728,16 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // tile loads issued from the slots of iteration j: K(j+2) and V(j+1)
   const char *lkb = t2.kb + (int64_t)t2.t * (kBN * KROW), *lvb = t1.vb + t1.t * (kBN * 2);
   uint32_t lvrs = t1.vrs2, lkd = lds0 + 2 * KT, lvd = lds0 + 3 * KT + 1 * VT;
+  set_voff(lvrs);
   for (;;) {
     // P of keys 0..31 of tile j; scores of keys 32..63 of tile j come next
-    sub_tile(kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, true, lkb, lkd, lvb,
-             lvrs, lvd);
+    sub_tile(sA, sB, kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, true, lkb,
+             lkd, lvb, lvd);
     // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 come next
     // (after the last tile they read a stale in-bounds buffer and are unused)
     const bool more = j + 1 < a.ntiles;
-    sub_tile(kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, false, lkb,
-             lkd, lvb, lvrs, lvd);
+    sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, false,
+             lkb, lkd, lvb, lvd);
     if (!more) break;
     ++j;
     wait_vmem();     // this wave's loads of K(j+1), V(j) (tile numbers of the new j)
@@ -703,7 +756,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     lkb = sk.kb + (int64_t)sk.t * (kBN * KROW);
     lkd = lds0 + b2 * KT;
     lvb = sv.vb + sv.t * (kBN * 2);
-    lvrs = sv.vrs2;
+    if (sv.vrs2 != lvrs) {  // the value loads moved to a segment with another row stride
+      lvrs = sv.vrs2;
+      set_voff(lvrs);
+    }
     lvd = lds0 + 3 * KT + b1 * VT;
     if constexpr (I8) ks2 = load_ks(sk);
     sv = sk;
