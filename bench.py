@@ -303,7 +303,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
             "traffic": traffic,
-            "kernel": "attn_fwd_kernel<128, bf16>",
+            "kernel": "attn_fwd_kernel<128, bf16> + attn_merge_kernel<128> (split last round)",
             "flops_per_launch": ATTN_FLOPS,
             "kernel_ms": round(attn_ms, 4),
         }

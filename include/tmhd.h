@@ -72,6 +72,16 @@ typedef struct tmhd_attn_args {
   float scale;            /* softmax scale (head_dim ** -0.5 in the model) */
   int32_t n_segments;     /* 1..TMHD_MAX_SEGMENTS */
   tmhd_kv_segment seg[TMHD_MAX_SEGMENTS];
+  /*
+   * Optional scratch (NULL: none).  The work is one item per (head, 256-row
+   * query tile); when the items do not fill the last round of the device's
+   * CUs, the remaining items are split into key ranges whose partial results
+   * go here and are merged by a second kernel on the same stream.  Without it
+   * (or with fewer bytes than tmhd_attn_split_workspace_bytes) every item runs
+   * whole.  Calls that share a workspace must be ordered (same stream).
+   */
+  void *split_workspace;
+  int64_t split_workspace_bytes;
 } tmhd_attn_args;
 
 /*
@@ -109,6 +119,14 @@ const char *tmhd_last_error(void);
  * are read in place.
  */
 int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream);
+
+/*
+ * Bytes of split_workspace that let every attention call with this head_dim
+ * on the current device split its last round (0 for an unsupported
+ * head_dim).  Has no counterpart in the reference: the reference's SDPA /
+ * SageAttention calls manage their own scratch.
+ */
+int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim);
 
 /*
  * INT8-QK streaming attention: int8 Q.K^T (int32 accumulate) dequantised by

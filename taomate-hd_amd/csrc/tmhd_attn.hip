@@ -93,6 +93,11 @@ struct KArgs {
   float c;  // softmax scale * log2(e)
   int32_t nseg;
   int32_t ntiles;  // sum of seg[].ntiles
+  // Items (head, query tile) [0, full) run whole, one per workgroup; the
+  // remaining ones run as nsplit key ranges each, whose partial results
+  // (per workgroup: [kBM][D] normalised O, then [kBM] log2-sum-exp) go to ws.
+  int32_t full, nsplit;
+  float *ws;
   Seg seg[kMaxSeg];
 };
 
@@ -133,6 +138,15 @@ __device__ __forceinline__ void stream_set(Stream &S, const KArgs &a, int h, int
   S.vb = (const char *)(G.vt + (int64_t)h * G.vhs);
   S.vrs2 = (uint32_t)G.vrs * 2u;
   S.ks = I8 ? G.ks + (int64_t)h * G.kshs : nullptr;
+}
+
+// Tile gt of the concatenated segments.
+template <bool I8>
+__device__ __forceinline__ void stream_seek(Stream &S, const KArgs &a, int h, int gt) {
+  int s = 0;
+  while (s + 1 < a.nseg && gt >= a.seg[s].ntiles) gt -= a.seg[s++].ntiles;
+  stream_set<I8>(S, a, h, s);
+  S.t = gt;
 }
 
 // Next tile; the last tile of the last segment repeats (loads of a repeated
@@ -403,7 +417,17 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   __shared__ __attribute__((aligned(1024))) char smem[3 * KT + 3 * VT];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
 
-  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
+  // item L, whole or key-tile range [t_begin, t_begin + cnt) of part `part`
+  int L, part = -1, t_begin = 0, cnt = a.ntiles;
+  if ((int)blockIdx.x < a.full) {
+    L = xcd_logical_id(blockIdx.x, a.full);
+  } else {
+    const int tb = blockIdx.x - a.full, item = tb / a.nsplit;
+    L = a.full + item;
+    part = tb - item * a.nsplit;
+    t_begin = a.ntiles * part / a.nsplit;
+    cnt = a.ntiles * (part + 1) / a.nsplit - t_begin;
+  }
   const int h = L / a.nqt;
   const int qt = L - h * a.nqt;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
@@ -545,7 +569,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 
   // ---- prologue: K(0..2), V(0..1) resident; S = scores of sub-tile 0 (minus m)
   Stream t0, t1, t2, t3;
-  stream_set<I8>(t0, a, h, 0);
+  stream_seek<I8>(t0, a, h, t_begin);
   t1 = t0;
   stream_next<I8>(t1, a, h);
   t2 = t1;
@@ -735,7 +759,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
              lkd, lvb, lvd);
     // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 come next
     // (after the last tile they read a stale in-bounds buffer and are unused)
-    const bool more = j + 1 < a.ntiles;
+    const bool more = j + 1 < cnt;
     sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, false,
              lkb, lkd, lvb, lvd);
     if (!more) break;
@@ -773,6 +797,27 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
     for (int db = 0; db < DB; ++db) opin(hf * DB + db, o[hf][db]);
+  if (part >= 0) {
+    // key range of a split item: normalised partial O and its log2-sum-exp
+    float *wo = a.ws + (int64_t)(blockIdx.x - a.full) * (kBM * D + kBM);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
+      const float inv = 1.0f / lt;
+      const int rl = w * kQW + hf * 32 + lr;  // row within the item
+      if (q0 + hf * 32 + lr < a.lq) {
+        float *op = wo + rl * D + 4 * g;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            *(f32x4 *)(op + db * 32 + 8 * u) = f32x4{o[hf][db][4 * u] * inv, o[hf][db][4 * u + 1] * inv,
+                                                     o[hf][db][4 * u + 2] * inv, o[hf][db][4 * u + 3] * inv};
+        if (g == 0) wo[kBM * D + rl] = mref[hf] + __log2f(lt);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf) {
     const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
@@ -793,7 +838,63 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   }
 }
 
+// Merge of split items: O = sum_p 2^(lse_p - lse) O_p with lse = log2 sum_p
+// 2^lse_p (the partial O_p are normalised).  One thread per 4 columns of a
+// row; item i of the split ones owns workspace blocks [i * nsplit, (i+1) * nsplit).
+template <int D>
+__global__ void __launch_bounds__(256) attn_merge_kernel(const KArgs a) {
+  constexpr int CG = D / 4, RPB = 256 / CG;  // column groups per row, rows per block
+  const int item = blockIdx.x / (kBM / RPB);
+  const int rl = (blockIdx.x - item * (kBM / RPB)) * RPB + threadIdx.x / CG;
+  const int cg = threadIdx.x % CG;
+  const int L = a.full + item, h = L / a.nqt, qt = L - h * a.nqt;
+  const int ql = qt * kBM + rl;
+  if (ql >= a.lq) return;
+  constexpr int64_t slot = kBM * D + kBM;
+  const float *base = a.ws + (int64_t)item * a.nsplit * slot;
+  float m = -INFINITY;
+  for (int p = 0; p < a.nsplit; ++p) m = fmaxf(m, base[p * slot + kBM * D + rl]);
+  float wsum = 0.0f;
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int p = 0; p < a.nsplit; ++p) {
+    const float wp = __builtin_amdgcn_exp2f(base[p * slot + kBM * D + rl] - m);
+    wsum += wp;
+    acc += wp * *(const f32x4 *)(base + p * slot + rl * D + 4 * cg);
+  }
+  const float inv = 1.0f / wsum;
+  const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
+  uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * cg;
+  *(i32x2 *)op = i32x2{(int)pack_bf16x2(acc[0] * inv, acc[1] * inv), (int)pack_bf16x2(acc[2] * inv, acc[3] * inv)};
+}
+
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+int64_t split_slot_bytes(int D) { return (int64_t)kBM * (D + 1) * 4; }
+
+// Key ranges per remaining item: as many as fit the CUs the whole items leave
+// free in the last round, at most 8, each at least 4 tiles long.
+int choose_split(int items, int cus, int ntiles) {
+  if (cus <= 0) return 1;
+  const int rem = items % cus;
+  if (rem == 0) return 1;
+  int n = cus / rem;
+  n = n < 8 ? n : 8;
+  n = n < ntiles / 4 ? n : ntiles / 4;
+  return n > 1 ? n : 1;
+}
 
 int build_kargs(const tmhd_attn_args *args, const tmhd_qk_quant *qq, bool i8, KArgs *k) {
   if (!args) return set_error(TMHD_ERR_INVALID, "attention: null args");
@@ -808,6 +909,8 @@ int build_kargs(const tmhd_attn_args *args, const tmhd_qk_quant *qq, bool i8, KA
   if (!i8 && (!args->q || !aligned(args->q, 16) || args->q_token_stride % 8 || args->q_head_stride % 8))
     return set_error(TMHD_ERR_INVALID, "attention: query pointer/strides must be 16-byte aligned");
   const int nqt = (args->lq + kBM - 1) / kBM;
+  if (args->split_workspace && (!aligned(args->split_workspace, 16) || args->split_workspace_bytes < 0))
+    return set_error(TMHD_ERR_INVALID, "attention: split workspace must be 16-byte aligned");
   *k = KArgs{};
   k->q = (const uint16_t *)args->q;
   k->qts = args->q_token_stride;
@@ -873,18 +976,48 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   int st = build_kargs(args, qq, I8, &k);
   if (st) return st;
   if (args->lq == 0) return TMHD_OK;
-  const int64_t grid = (int64_t)k.nqt * k.heads;
-  if (grid > 0x7fffffff) return set_error(TMHD_ERR_UNSUPPORTED, "attention: grid too large");
+  const int64_t items = (int64_t)k.nqt * k.heads;
+  if (items > 0x3fffffff) return set_error(TMHD_ERR_UNSUPPORTED, "attention: grid too large");
+  // split the items of the last, partial round into key ranges when a workspace is given
+  k.full = (int)items;
+  k.nsplit = 1;
+  int rem = 0;
+  if (args->split_workspace) {
+    const int cus = device_cus();
+    const int n = choose_split((int)items, cus, k.ntiles);
+    rem = n > 1 ? (int)(items % cus) : 0;
+    if (n > 1 && args->split_workspace_bytes >= (int64_t)rem * n * split_slot_bytes(args->head_dim)) {
+      k.full = (int)items - rem;
+      k.nsplit = n;
+      k.ws = (float *)args->split_workspace;
+    } else {
+      rem = 0;
+    }
+  }
+  const unsigned grid = (unsigned)(k.full + (int64_t)rem * k.nsplit);
   hipStream_t s = (hipStream_t)stream;
   if (args->head_dim == 128)
-    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3(grid), dim3(kWaves * 64), 0, s, k);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3((unsigned)grid), dim3(kWaves * 64), 0, s, k);
-  return check_launch(I8 ? "tmhd_attn_fwd_i8qk" : "tmhd_attn_fwd_bf16");
+    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3(grid), dim3(kWaves * 64), 0, s, k);
+  const char *what = I8 ? "tmhd_attn_fwd_i8qk" : "tmhd_attn_fwd_bf16";
+  int st2 = check_launch(what);
+  if (st2 || rem == 0) return st2;
+  const unsigned mgrid = (unsigned)rem * (kBM / (256 / (args->head_dim / 4)));
+  if (args->head_dim == 128)
+    hipLaunchKernelGGL((attn_merge_kernel<128>), dim3(mgrid), dim3(256), 0, s, k);
+  else
+    hipLaunchKernelGGL((attn_merge_kernel<64>), dim3(mgrid), dim3(256), 0, s, k);
+  return check_launch(what);
 }
 
 }  // namespace
 }  // namespace tmhd
+
+extern "C" int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim) {
+  if (head_dim != 64 && head_dim != 128) return 0;
+  return (int64_t)tmhd::device_cus() * tmhd::split_slot_bytes(head_dim);
+}
 
 extern "C" int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream) {
   return tmhd::launch_attn<false>(args, nullptr, stream);

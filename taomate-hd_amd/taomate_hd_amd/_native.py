@@ -53,6 +53,8 @@ class AttnArgs(ctypes.Structure):
         ("scale", c_float),
         ("n_segments", c_int32),
         ("seg", KVSegment * MAX_SEGMENTS),
+        ("split_workspace", c_void_p),
+        ("split_workspace_bytes", c_int64),
     ]
 
 
@@ -75,6 +77,7 @@ class QKQuant(ctypes.Structure):
 _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "tmhd_version": (c_char_p, []),
     "tmhd_last_error": (c_char_p, []),
+    "tmhd_attn_split_workspace_bytes": (c_int64, [c_int32]),
     "tmhd_attn_fwd_bf16": (c_int, [POINTER(AttnArgs), c_void_p]),
     "tmhd_attn_fwd_i8qk": (c_int, [POINTER(AttnArgs), POINTER(QKQuant), c_void_p]),
     "tmhd_qk_smooth_quant": (c_int, [POINTER(AttnArgs), POINTER(QKQuant), c_void_p]),

@@ -82,6 +82,24 @@ class QKQuantWorkspace:
         return qq, views
 
 
+_SPLIT_WORKSPACES: dict[tuple[Any, ...], Any] = {}
+
+
+def split_workspace(torch: Any, device: Any, head_dim: int) -> Any:
+    """Scratch for the key-range split of an attention call's last round.
+
+    One uint8 buffer per (device, stream), grown to what the library asks for
+    on that device; calls on one stream are ordered, so they share it.
+    """
+    need = int(_native.load().tmhd_attn_split_workspace_bytes(int(head_dim)))
+    key = (str(device), _native.stream_ptr(torch, device))
+    buf = _SPLIT_WORKSPACES.get(key)
+    if buf is None or buf.numel() < need:
+        buf = torch.empty(max(need, 1), dtype=torch.uint8, device=device)
+        _SPLIT_WORKSPACES[key] = buf
+    return buf
+
+
 def _validate_tokens_major(torch: Any, tensor: Any, name: str) -> None:
     _native.require_device_tensor(torch, tensor, name)
     if tensor.dtype != torch.bfloat16 or tensor.ndim != 3 or tensor.stride(2) != 1:
@@ -102,6 +120,7 @@ def segment_attention(
     o_rows: Any | None = None,
     o_row0: int = 0,
     workspace: QKQuantWorkspace | None = None,
+    split: bool = True,
     return_quant: bool = False,
     timer: ComponentTimer | None = None,
 ) -> Any:
@@ -109,7 +128,9 @@ def segment_attention(
 
     Query row ``i`` is ``query[q_rows[i]]`` (or ``query[q_row0 + i]``); its
     output goes to ``out[o_rows[i]]`` (or ``out[o_row0 + i]``).  Without
-    ``out`` a new ``[lq, H, D]`` tensor is returned.
+    ``out`` a new ``[lq, H, D]`` tensor is returned.  ``split`` lets the
+    library run the items of a partial last round as key ranges (merged on
+    the same stream); results agree with the unsplit run to fp32 rounding.
     """
     if backend not in BACKENDS:
         raise ValueError(f"unknown attention backend {backend!r}")
@@ -169,6 +190,10 @@ def segment_attention(
         args.seg[i] = s.to_segment()
     lib = _native.load()
     stream = _native.stream_ptr(torch, query.device)
+    if split and lq:
+        ws = split_workspace(torch, query.device, head_dim)
+        args.split_workspace = _native.ptr(ws)
+        args.split_workspace_bytes = int(ws.numel())
     if backend == "bf16":
         with maybe_region(timer, "attention"):
             status = lib.tmhd_attn_fwd_bf16(args, stream)

@@ -17,7 +17,7 @@ HEADER = REPO / "include" / "tmhd.h"
 
 def _declared_symbols() -> list[str]:
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|const char \*)\s*(tmhd_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|const char \*)\s*(tmhd_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
 
     lib = _native.load()
     declared = _declared_symbols()
-    assert len(declared) == 10
+    assert len(declared) == 11
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED_SYMBOLS)

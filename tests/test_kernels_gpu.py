@@ -162,6 +162,41 @@ def test_i8qk_attention(torch_mod, dev, heads, dim, lq, splits):
     assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("backend", ["bf16", "i8qk"])
+@pytest.mark.parametrize(
+    "heads,dim,lq,splits",
+    [
+        (40, 128, 1792, [1000, 1560]),  # 280 (head, query-tile) items: a full round of 256 CUs plus 24
+        (5, 64, 600, [64, 900, 3]),  # 15 items on 256 CUs: every item split, ranges cross segments
+    ],
+)
+def test_split_last_round_matches_whole_items(torch_mod, dev, backend, heads, dim, lq, splits):
+    """Items of a partial last round run as key ranges merged by log2-sum-exp;
+    the result matches the unsplit run (and, for BF16, the fp64 oracle on the
+    heads that were split)."""
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    n = sum(splits)
+    q = randn_bf16((lq, heads, dim), 40)
+    k = randn_bf16((n, heads, dim), 41, offset=key_offset(heads, dim, 43))
+    v = randn_bf16((n, heads, dim), 42)
+    views = _slots(torch, dev, k, v, splits)
+    qd = to_dev(q, dev)
+    whole = segment_attention(torch, qd, views, scale=dim ** -0.5, backend=backend, split=False)
+    split = segment_attention(torch, qd, views, scale=dim ** -0.5, backend=backend, split=True)
+    torch.cuda.synchronize()
+    a, b = bf16.from_torch(whole), bf16.from_torch(split)
+    # same scores and probabilities, other summation order: at most a few bf16 ulps apart
+    mx, mean = err_stats(b, a)
+    assert mx <= 1.6e-2 and mean <= 2e-4, (mx, mean)
+    if backend == "bf16":
+        hs = list(range(max(0, heads - 4), heads))  # the last items are the split ones
+        want = oatt.attention_fp64(q[:, hs], k[:, hs], v[:, hs], dim ** -0.5)
+        mx, mean = err_stats(b[:, hs], want)
+        assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+
+
 def test_token_quant_bit_exact(torch_mod, dev):
     torch = torch_mod
     from taomate_hd_amd import quant
