@@ -212,7 +212,7 @@ def read_traffic():
         return None
     for line in TRAFFIC_PROFILE.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1].strip())
+            return float(line.split(":", 1)[1].split()[0])
     return None
 
 

@@ -35,9 +35,11 @@
 //   exceeds it by 2^8 (lazy rescale); P values stay <= 2^8.
 //
 // Pipeline: a tile is two 32-key sub-tiles; each sub-tile is one basic block
-// of fenced slots, each slot one LDS operand read (issued three slots ahead)
-// and two MFMAs (one per query half) plus its share of the other work, spread
-// by a compile-time plan that evens out the instructions per slot:
+// of fenced slots, each slot one LDS operand read (issued four slots ahead)
+// and two MFMAs (one per query half).  Issuing an MFMA holds the wave for
+// about half of the MFMA's 32 cycles, so every MFMA is followed by its own
+// share of the other work, spread by a compile-time plan that evens out the
+// issue cycles between consecutive MFMAs:
 //   exp2 / pack / row-sum of P(s)      under the score MFMAs of sub-tile s+1
 //                                      and the first P.V MFMAs of sub-tile s,
 //   scaling and row max of S(s+1)      under the later P.V MFMAs of sub-tile s,
@@ -168,12 +170,12 @@ __device__ __forceinline__ void stream_next(Stream &S, const KArgs &a, int h) {
 // SIMD, up to 512 registers) while scores and probabilities stay in VGPRs.
 // The compiler does not see through the asm, so the hazards it would resolve
 // for builtins are resolved by construction in the kernel:
-//   * VALU write -> MFMA operand read needs 2 wait states: the first MFMA that
-//     reads a freshly packed P group uses the *_fresh form (s_nop 1);
+//   * VALU write -> MFMA operand read needs 2 wait states: a P.V MFMA whose
+//     P group was packed in front of the previous MFMA carries an s_nop 1;
 //   * MFMA result -> VALU read (12 wait states for either MFMA): score results
-//     are first read behind an s_nop 9 in the second output slot, which names
-//     them so that no read moves above it; AGPR accumulators are read only
-//     after mfma_drain();
+//     are first read behind an s_nop 10 after the second output MFMA, which
+//     names them so that no read moves above it; AGPR accumulators are read
+//     only after mfma_drain();
 //   * accvgpr write (rescale) -> MFMA accumulate: s_nop 2 after the rescale;
 //   * the rescale itself reads each AGPR after mfma_drain();
 //   * back-to-back accumulation into the same registers needs no wait states.
@@ -353,37 +355,56 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
-// Work plan of one sub-tile's slots, fixed at compile time.  Units:
-//   P(u): exp2 / bf16 pack / row sum of pair u % 8 (keys 2q, 2q+1) of query
-//         half u / 8 of the current sub-tile; pairs 0..3 feed the first P.V
-//         k-step (slot nqk), pairs 4..7 the second (slot nqk + db);
+// Work plan of one sub-tile, fixed at compile time.  The sub-tile issues
+// 2 * ns MFMAs (two per slot, one per query half); region r is the code in
+// front of MFMA r.  Issuing an MFMA holds the wave for about 16 of the MFMA's
+// 32 cycles, so each region has about 16 cycles for other instructions before
+// the matrix core idles.  Units, with their issue cycles:
+//   E(u): the two exp2 of pair u % 8 (keys 2q, 2q+1) of query half u / 8 of
+//         the current sub-tile (8 each);
+//   C(u): their bf16 pack and row-sum adds (4 each), at or after E(u) and at
+//         least one MFMA before the P.V MFMA that reads the pack;
 //   M(u): INT8 dequantisation and row maximum of pair u % 8, half u / 8 of
-//         the next sub-tile's scores, after its score chain (slot nqk + 1 on);
-//   L(n): tile load n, in the first `lwin` slots.
-// Each slot starts at the cost of its operand read and wait; every unit goes
-// to the cheapest slot of its window (the earliest on ties).
+//         the next sub-tile's scores, after the score-read guard;
+//   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions.
+// Every region starts with its share of the fixed work (the operand read of
+// odd regions, the wait in front of each slot's first MFMA); each unit goes
+// to the cheapest region of its window (the earliest on ties).
 struct SlotPlan {
-  int p[16], m[16], l[16];
+  int e[16], c[16], m[16], l[16];
 };
-constexpr int plan_put(int (&cost)[32], int lo, int hi, int c) {
+constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   int best = lo;
   for (int i = lo + 1; i <= hi; ++i)
     if (cost[i] < cost[best]) best = i;
   cost[best] += c;
   return best;
 }
+constexpr int kGuardRegionOffset = 1;  // score-read guard in region 2 * nqk + 1
 constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i8) {
   SlotPlan s{};
-  int cost[32] = {};
-  const int ns = nqk + npv;
-  for (int i = 0; i < ns; ++i) cost[i] = 2;
+  int cost[64] = {};
+  const int ns = nqk + npv, nr = 2 * ns;
+  for (int i = 0; i < ns; ++i) {
+    cost[2 * i] += 4;
+    cost[2 * i + 1] += 4;
+  }
+  cost[2 * nqk + kGuardRegionOffset] += 11;
   for (int q = 0; q < 4; ++q)
-    for (int hf = 0; hf < 2; ++hf) s.p[hf * 8 + q] = plan_put(cost, 0, nqk - 1, 6);
+    for (int hf = 0; hf < 2; ++hf) {
+      const int u = hf * 8 + q, dl = 2 * nqk + hf - 1;
+      s.e[u] = plan_put(cost, 0, dl, 16);
+      s.c[u] = plan_put(cost, s.e[u], dl, 12);
+    }
   for (int q = 0; q < 8; ++q)
-    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, nqk + 1, ns - 1, i8 ? 3 : 1);
+    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 12 : 4);
   for (int q = 4; q < 8; ++q)
-    for (int hf = 0; hf < 2; ++hf) s.p[hf * 8 + q] = plan_put(cost, 0, nqk + db - 1, 6);
-  for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 3) : -1;
+    for (int hf = 0; hf < 2; ++hf) {
+      const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
+      s.e[u] = plan_put(cost, 0, dl, 16);
+      s.c[u] = plan_put(cost, s.e[u], dl, 12);
+    }
+  for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 8) : -1;
   return s;
 }
 
@@ -405,9 +426,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   constexpr int NQK = QST;     // score slots per 32-key sub-tile (one K operand, two MFMAs)
   constexpr int NPV = 2 * DB;  // output slots per sub-tile (one V operand, two MFMAs)
   constexpr int NS = NQK + NPV;
-  constexpr int LA = NQK < 3 ? NQK : 3;  // LDS operand reads in flight ahead of their slot
+  constexpr int LA = NQK < 4 ? NQK : 4;  // LDS operand reads in flight ahead of their slot
   static_assert(LA <= NQK, "the reads prefetched for the next sub-tile are score-slot reads");
-  static_assert(NS <= 32 && NPV >= 2, "slot plan bounds");
+  static_assert(NS <= 32 && NPV >= 4, "slot plan bounds");
 
   // LDS: three K tiles, then three V tiles (tile t lives in buffer t % 3).  A
   // 16-lane ds_read_b128 phase reads one 16-byte chunk of 16 consecutive rows;
@@ -501,7 +522,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // load n of a tile: K blocks first (n < KWL), then V blocks
   constexpr int NLD = KWL + VWL;
   static_assert(NLD <= 16, "slot plan bounds");
-  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, 3 * NS / 4, I8);  // sub-tiles with tile loads
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, 3 * NS / 2, I8);  // sub-tiles with tile loads
   constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8);               // sub-tiles without
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
@@ -634,10 +655,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 
   int j = 0, b0 = 0, b1 = 1, b2 = 2;  // LDS buffers of tiles j, j+1, j+2
 
-  // One 32-key sub-tile, software-pipelined by hand in NS slots fenced so
-  // that the compiler keeps their order.  Slot i issues the LDS operand read
-  // of slot i + LA, the units the slot plan gives it, then its two MFMAs (one
-  // per query half):
+  // One 32-key sub-tile, software-pipelined by hand in NS slots of two MFMAs
+  // (one per query half), each MFMA fenced with the units the plan puts in
+  // front of it so that the compiler keeps their order.  Slot i also issues
+  // the LDS operand read of slot i + LA:
   //   slots [0, NQK):  scores of the next sub-tile, K rows at kb (k-step st = i);
   //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile, V chunks at vb.
   // sc: scores (minus m) of the current sub-tile; sn: receives those of the
@@ -647,7 +668,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // the operands of the first LA slots, read by the previous sub-tile; on
   // return, those of the next sub-tile (K rows at kbn).
   auto sub_tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], uint32_t kb, uint32_t vb, uint32_t kbn, i32x4 (&pre)[LA],
-                      int nvs, float ctn, bool live, bool loads, const char *lkb, uint32_t lkd, const char *lvb,
+                      int nvs, float ctn, bool live, auto loads_c, const char *lkb, uint32_t lkd, const char *lvb,
                       uint32_t lvd) {
     const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
     auto read_op = [&](int i) -> i32x4 {
@@ -662,59 +683,73 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     float lm[2] = {-INFINITY, -INFINITY};
 #pragma unroll
     for (int i = 0; i < LA; ++i) ops[i] = pre[i];
+    float pe[2][8][2];  // exponentials of the current sub-tile, between their E and C units
 #pragma clang loop unroll(full)
-    for (int i = 0; i < NS; ++i) {
-      const SlotPlan &pl = loads ? PL : PN;
-      if (i + LA < NS)
-        ops[i + LA] = read_op(i + LA);
-      else
-        pre[i + LA - NS] = lds_read(kbn + (i + LA - NS) * 32);
+    for (int r = 0; r < 2 * NS; ++r) {
+      const int i = r >> 1, hr = r & 1;  // slot, query half of MFMA r
+      constexpr bool loads = decltype(loads_c)::value;
+      constexpr SlotPlan pl = loads ? PL : PN;
+      if (hr == 1) {
+        if (i + LA < NS)
+          ops[i + LA] = read_op(i + LA);
+        else
+          pre[i + LA - NS] = lds_read(kbn + (i + LA - NS) * 32);
+      }
       if (loads)
 #pragma unroll
         for (int n = 0; n < NLD; ++n)
-          if (pl.l[n] == i) load_one(n, lkb, lkd, lvb, lvd);
+          if (pl.l[n] == r) load_one(n, lkb, lkd, lvb, lvd);
 #pragma unroll
       for (int u = 0; u < 16; ++u)
-        if (pl.p[u] == i) {
+        if (pl.e[u] == r) {
           const int hf = u >> 3, q = u & 7;
-          const float e0 = __builtin_amdgcn_exp2f(sc[hf][2 * q]), e1 = __builtin_amdgcn_exp2f(sc[hf][2 * q + 1]);
-          pk[hf][q >> 2][q & 3] = (int)pack_bf16x2(e0, e1);
-          ts[hf] += e0;
-          ts[hf] += e1;
-          asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this slot
+          pe[hf][q][0] = __builtin_amdgcn_exp2f(sc[hf][2 * q]);
+          pe[hf][q][1] = __builtin_amdgcn_exp2f(sc[hf][2 * q + 1]);
+          asm volatile("" : "+v"(pe[hf][q][0]), "+v"(pe[hf][q][1]));  // keeps them in this region
         }
-      if (i == NQK + 1) {
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.c[u] == r) {
+          const int hf = u >> 3, q = u & 7;
+          int pr = (int)pack_bf16x2(pe[hf][q][0], pe[hf][q][1]);
+          ts[hf] += pe[hf][q][0];
+          ts[hf] += pe[hf][q][1];
+          asm volatile("" : "+v"(pr), "+v"(ts[hf]));  // keeps the pack and the row sum in this region
+          pk[hf][q >> 2][q & 3] = pr;
+        }
+      if (r == 2 * NQK + kGuardRegionOffset) {
         // first reads of the next sub-tile's scores: at least 12 wait states
-        // after the last score MFMA (slot NQK's two MFMAs, its operand read and
-        // wait, and these 10); naming the results keeps every read below
+        // after the last score MFMA (the MFMA in front of this region and
+        // these 10); naming the results keeps every read below
         if constexpr (I8)
-          asm volatile("s_nop 9" : "+v"(sni[0]), "+v"(sni[1]));
+          asm volatile("s_nop 10" : "+v"(sni[0]), "+v"(sni[1]));
         else
-          asm volatile("s_nop 9" : "+v"(sn[0]), "+v"(sn[1]));
+          asm volatile("s_nop 10" : "+v"(sn[0]), "+v"(sn[1]));
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u)
-        if (pl.m[u] == i) {
-          const int hf = u >> 3, r = (u & 7) * 2;
+        if (pl.m[u] == r) {
+          const int hf = u >> 3, rr = (u & 7) * 2;
           if constexpr (I8) {
-            sn[hf][r] = fmaf(__int_as_float(sni[hf][r]), ctn, nbn[hf]);
-            sn[hf][r + 1] = fmaf(__int_as_float(sni[hf][r + 1]), ctn, nbn[hf]);
+            sn[hf][rr] = fmaf(__int_as_float(sni[hf][rr]), ctn, nbn[hf]);
+            sn[hf][rr + 1] = fmaf(__int_as_float(sni[hf][rr + 1]), ctn, nbn[hf]);
           }
-          lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][r], sn[hf][r + 1]));
-          asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this slot
+          lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][rr], sn[hf][rr + 1]));
+          asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this region
         }
+      __builtin_amdgcn_sched_barrier(0);
       if (i < NQK) {
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          if constexpr (I8)
-            qk_i8(hf * QST + i, i == 0, sni[hf], ops[i], qv[hf][i], magic);
-          else
-            qk_bf16(hf * QST + i, i == 0, sn[hf], ops[i], qv[hf][i], negm[hf]);
-        }
+        if constexpr (I8)
+          qk_i8(hr * QST + i, i == 0, sni[hr], ops[i], qv[hr][i], magic);
+        else
+          qk_bf16(hr * QST + i, i == 0, sn[hr], ops[i], qv[hr][i], negm[hr]);
       } else {
         const int p = i - NQK, st = p / DB, db = p % DB;
+        // the P group read here was packed in the region in front of the previous MFMA
+        bool fresh = false;
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) pv(hf * DB + db, db == 0, o[hf][db], ops[i], pk[hf][st]);
+        for (int q = 4 * st; q < 4 * st + 4; ++q) fresh = fresh || pl.c[hr * 8 + q] >= r - 1;
+        pv(hr * DB + db, fresh, o[hr][db], ops[i], pk[hr][st]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -755,12 +790,12 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   set_voff(lvrs);
   for (;;) {
     // P of keys 0..31 of tile j; scores of keys 32..63 of tile j come next
-    sub_tile(sA, sB, kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, true, lkb,
+    sub_tile(sA, sB, kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, std::true_type{}, lkb,
              lkd, lvb, lvd);
     // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 come next
     // (after the last tile they read a stale in-bounds buffer and are unused)
     const bool more = j + 1 < cnt;
-    sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, false,
+    sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, std::false_type{},
              lkb, lkd, lvb, lvd);
     if (!more) break;
     ++j;
