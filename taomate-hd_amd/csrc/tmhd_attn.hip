@@ -11,7 +11,10 @@
 //   workgroup = 4 waves = 256 query rows of one head, one workgroup per CU and
 //   one wave per SIMD.  Each wave owns 64 query rows (two 32-row halves) and
 //   keeps their query operands and fp32 output accumulators in AGPRs at fixed
-//   registers, the scores, probabilities and online-softmax state in VGPRs.
+//   registers, the score chain starts (BF16: -m per half; INT8: the magic
+//   constant) at fixed VGPRs v[224:255], and the scores, probabilities and
+//   online-softmax state in the other VGPRs.  Fixed registers keep the
+//   compiler from moving these long-lived values around the loop.
 //   Keys and values stream through LDS in 64-token tiles, triple-buffered
 //   (tile t in buffer t % 3) and loaded with global_load_lds_dwordx4 (no
 //   VGPR staging): K runs two tiles ahead of the tile being finished, V one.
@@ -210,13 +213,17 @@ __device__ __forceinline__ void qpin(int qb, i32x4 &q) {
 #undef TMHD_QBLK
 #define TMHD_QBLK(QB, LO, HI)                                                                                      \
   case QB:                                                                                                         \
-    if (first)                                                                                                     \
-      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "v"(c));       \
+    if (first && hf == 0)                                                                                          \
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "{v[224:239]}"(c)); \
+    else if (first)                                                                                                \
+      asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "{v[240:255]}"(c)); \
     else                                                                                                           \
       asm("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q));                \
     break;
-// S^T (+)= K Q^T for one k-step: `first` starts the chain at c.
-__device__ __forceinline__ void qk_bf16(int qb, bool first, f32x16 &d, i32x4 k, const i32x4 &q, const f32x16 &c) {
+// S^T (+)= K Q^T for one k-step of query half hf: `first` starts the chain at
+// c, which lives in v[224:239] (hf 0) or v[240:255] (hf 1).
+__device__ __forceinline__ void qk_bf16(int qb, int hf, bool first, f32x16 &d, i32x4 k, const i32x4 &q,
+                                        const f32x16 &c) {
   switch (qb) {
     TMHD_QBLK(0, 128, 131)
     TMHD_QBLK(1, 132, 135)
@@ -240,11 +247,11 @@ __device__ __forceinline__ void qk_bf16(int qb, bool first, f32x16 &d, i32x4 k, 
 #define TMHD_QBLK(QB, LO, HI)                                                                                      \
   case QB:                                                                                                         \
     if (first)                                                                                                     \
-      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "v"(c));         \
+      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "{v[224:239]}"(c)); \
     else                                                                                                           \
       asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q));                  \
     break;
-// INT8 form: the chain starts at the accumulator vector c.
+// INT8 form: the chain starts at the accumulator vector c, in v[224:239].
 __device__ __forceinline__ void qk_i8(int qb, bool first, i32x16 &d, i32x4 k, const i32x4 &q, const i32x16 &c) {
   switch (qb) {
     TMHD_QBLK(0, 128, 131)
@@ -309,6 +316,14 @@ __device__ __forceinline__ void opin(int b, f32x16 &o) {
   }
 }
 #undef TMHD_OPIN
+// Declares the score chain start of query half hf as live in its VGPRs.
+__device__ __forceinline__ void npin(int hf, f32x16 &c) {
+  if (hf == 0)
+    asm volatile("" : "+{v[224:239]}"(c));
+  else
+    asm volatile("" : "+{v[240:255]}"(c));
+}
+__device__ __forceinline__ void npin(i32x16 &c) { asm volatile("" : "+{v[224:239]}"(c)); }
 // o *= alpha for block b, in place in its AGPRs (read, multiply, write back).
 #define TMHD_RS(N) "v_accvgpr_read_b32 %1, a" #N "\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 a" #N ", %1\n\t"
 #define TMHD_RS4(A, B, C, D) TMHD_RS(A) TMHD_RS(B) TMHD_RS(C) TMHD_RS(D)
@@ -494,6 +509,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   i32x16 magic;  // INT8 score accumulator start
 #pragma unroll
   for (int r = 0; r < 16; ++r) magic[r] = kI8Magic;
+  if constexpr (I8) npin(magic);
 
   // per-lane LDS read offsets from smem (bytes; k-step, key half, buffer and db parts are uniform/immediate)
   const uint32_t kro = lr * KRS + g * 16;
@@ -560,12 +576,15 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   auto tile_valid = [](const Stream &S) { return min(S.tok - S.t * kBN, kBN); };
 
   // keys of a 32-key sub-tile at or beyond nvalid (relative to the sub-tile) -> -inf
+  // (element r of a lane holds key 8 (r / 4) + 4 g + r % 4; comparing the
+  // constant part with nvalid - 4 g keeps no per-element constants in registers)
   auto mask_sub = [&](f32x16 (&s)[2], int nvalid) {
+    const int t = nvalid - 4 * g;
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (8 * (r >> 2) + 4 * g + (r & 3) >= nvalid) s[hf][r] = -INFINITY;
+        if (8 * (r >> 2) + (r & 3) >= t) s[hf][r] = -INFINITY;
   };
   auto sub_max = [](const f32x16 &s) {
     float m = fmaxf(s[0], s[1]);
@@ -633,7 +652,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       for (int st = 0; st < QST; ++st) {
         const i32x4 kv = lds_read(kro + st * 32);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) qk_bf16(hf * QST + st, st == 0, sA[hf], kv, qv[hf][st], zero16);
+        for (int hf = 0; hf < 2; ++hf) {
+          if (st == 0) sA[hf] = zero16;
+          qk_bf16(hf * QST + st, hf, false, sA[hf], kv, qv[hf][st], zero16);
+        }
       }
       mfma_drain();
     }
@@ -644,6 +666,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       mref[hf] = fmaxf(lm, __shfl_xor(lm, 32));
       sA[hf] -= mref[hf];
       negm[hf] = -mref[hf];
+      if constexpr (!I8) npin(hf, negm[hf]);
     }
   }
   // load streams: K of tile j+3 and V of tile j+2, issued after the barrier of iteration j
@@ -742,7 +765,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         if constexpr (I8)
           qk_i8(hr * QST + i, i == 0, sni[hr], ops[i], qv[hr][i], magic);
         else
-          qk_bf16(hr * QST + i, i == 0, sn[hr], ops[i], qv[hr][i], negm[hr]);
+          qk_bf16(hr * QST + i, hr, i == 0, sn[hr], ops[i], qv[hr][i], negm[hr]);
       } else {
         const int p = i - NQK, st = p / DB, db = p % DB;
         // the P group read here was packed in the region in front of the previous MFMA
@@ -776,6 +799,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         sn[hf] -= delta;
         mref[hf] += delta;
         negm[hf] = -mref[hf];
+        if constexpr (!I8) npin(hf, negm[hf]);
       }
       asm volatile("s_nop 2" ::: "memory");
     }
