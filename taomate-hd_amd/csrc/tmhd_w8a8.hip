@@ -4,6 +4,8 @@
 // src/taomate_hd/inference/w8a8.py:67-73, 117-145, 175-179).
 #include <math.h>
 
+#include <type_traits>
+
 #include "tmhd_internal.h"
 
 namespace tmhd {
@@ -144,6 +146,8 @@ struct GArgs {
   int32_t m, n, k;
   int64_t lda, ldb, ldo;
   int32_t tm_count, tn_count;
+  int32_t vec_ok;  // bs 16-byte and bias 8-byte aligned: vector loads of 4 columns
+  int32_t st_ok;   // bf16 output rows 16-byte aligned: staged 16-byte stores
 };
 
 __device__ __forceinline__ int xcd_logical_id(int b, int G) {
@@ -296,6 +300,264 @@ gemm_i8_kernel(const GArgs ga) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// INT8 GEMM, one wave per SIMD: workgroup tile 256 (m) x 256 (n), 4 waves as
+// 2 (m) x 2 (n), each wave 128 x 128 (16 MFMA blocks, 256 int32 accumulators
+// per lane in AGPRs).  A 32-byte k-step reads 4 A and 4 B operands
+// (ds_read_b128) for 16 MFMAs; the next k-step's reads are issued under the
+// current one's MFMAs, one read per MFMA.
+// k-stages of 64 bytes (two k-steps) cycle through a 5-deep LDS ring (5 x 32
+// KiB, all of the CU's LDS) filled by global_load_lds_dwordx4, four stages
+// ahead.  Stage s has one barrier, after its k-step 0 (whose slots already
+// read k-step 1's operands): behind it, stage s+1 is complete for k-step 1 to
+// prefetch from, and stage s's slot is free for stage s+5, whose loads go out
+// under k-step 1's MFMAs.
+// LDS rows are 64 bytes (4 chunks); chunk c of row r sits at c ^ ((r >> 2) & 3),
+// so the 16 lanes of one ds_read_b128 phase (16 consecutive rows) hit 16
+// distinct 16-byte bank groups.
+constexpr int HBM_ = 256, HBN = 256, HKS = 64, HWAVES = 4, HRING = 5;
+constexpr int HSIDE = HBM_ * HKS;  // bytes of one operand's stage
+constexpr int HSTAGE = 2 * HSIDE;  // A then B
+constexpr int HLOADS = 2 * HSIDE / 1024 / HWAVES;  // 1 KiB wave loads per wave and stage
+
+__device__ __forceinline__ void hload_lds16(const void *base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
+}
+
+template <bool RAW>
+__global__ void __launch_bounds__(HWAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_i8_wave128_kernel(const GArgs ga) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char smem[HRING * HSTAGE];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;  // wave tile: a rows [wm*128, +128), b rows [wn*128, +128)
+  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
+  constexpr int GROUP = 8;  // 8 row tiles share each column sweep (L2 reuse)
+  const int per_group = GROUP * ga.tn_count;
+  const int grp = L / per_group;
+  const int first_tm = grp * GROUP;
+  const int gsize = min(ga.tm_count - first_tm, GROUP);
+  const int tm = first_tm + (L % per_group) % gsize;
+  const int tn = (L % per_group) / gsize;
+  const int m0 = tm * HBM_, n0 = tn * HBN;
+
+  // loads: 16 blocks of 1 KiB (16 rows of 64 B) per operand and stage; wave w
+  // loads blocks w, w + 4, w + 8, w + 12 of each.  Lane: row 16 blk + lane / 4,
+  // physical chunk lane % 4, logical chunk (lane % 4) ^ ((row >> 2) & 3) -- the
+  // same for all of the wave's blocks.
+  const int lch = (lane & 3) ^ ((lane >> 4) & 3);
+  uint32_t aoff[4], boff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (w + 4 * i) * 16 + (lane >> 2);
+    aoff[i] = (uint32_t)((int64_t)min(m0 + row, ga.m - 1) * ga.lda) + lch * 16;
+    boff[i] = (uint32_t)((int64_t)min(n0 + row, ga.n - 1) * ga.ldb) + lch * 16;
+  }
+  auto load_one = [&](int n, int kt, uint32_t stage) {
+    const int i = n & 3;
+    if (n < 4)
+      hload_lds16(ga.a + (int64_t)kt * HKS, aoff[i], stage + (w + 4 * i) * 1024);
+    else
+      hload_lds16(ga.b + (int64_t)kt * HKS, boff[i], stage + HSIDE + (w + 4 * i) * 1024);
+  };
+  // operand read offsets (k-step ks): row base + swizzled chunk 2 ks + g
+  const int x = (lr >> 2) & 3;
+  uint32_t ard[2], brd[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const uint32_t c = (uint32_t)(((2 * ks + g) ^ x) * 16);
+    ard[ks] = (uint32_t)((wm * 128 + lr) * HKS) + c;
+    brd[ks] = (uint32_t)(HSIDE + (wn * 128 + lr) * HKS) + c;
+  }
+  auto rd = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
+  // operand r of k-step ks in ring slot sb: r < 4: A block r, else B block r - 4
+  auto read_op = [&](int sb, int ks, int r) -> i32x4 {
+    if (r < 4) return rd(sb * HSTAGE + ard[ks] + r * 32 * HKS);
+    return rd(sb * HSTAGE + brd[ks] + (r - 4) * 32 * HKS);
+  };
+
+  i32x16 acc[4][4];  // [n block][m block], D[n][m]
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int nst = ga.k / HKS;
+  // prologue: stages 0..4 in flight (past the last stage the loads repeat it,
+  // into slots that are never read); stage 0 landed, then its k-step 0 operands
+#pragma unroll
+  for (int st = 0; st < HRING; ++st)
+#pragma unroll
+    for (int n = 0; n < HLOADS; ++n) load_one(n, min(st, nst - 1), lds0 + st * HSTAGE);
+  constexpr int VW0 = (HRING - 1) * HLOADS, VW1 = (HRING - 2) * HLOADS;  // loads that may stay in flight
+  static_assert(VW0 < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (VW0 & 15) | ((VW0 >> 4) << 14));
+  __syncthreads();
+  i32x4 cur[8], nxt[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) cur[r] = read_op(0, 0, r);
+
+  // one stage in ring slot sb: k-steps 0 and 1; stage s + 1 is in slot (sb + 1) % HRING
+  auto stage = [&](auto sb_c, int s) {
+    constexpr int sb = decltype(sb_c)::value, sn = (sb + 1) % HRING;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks == 1) {
+        // stage s + 1 landed (stages s + 2 .. s + HRING - 1 may stay in
+        // flight) and visible; slot sb free for stage s + HRING
+        __builtin_amdgcn_s_waitcnt(0x0f70 | (VW1 & 15) | ((VW1 >> 4) << 14));
+        __syncthreads();
+      }
+#pragma unroll
+      for (int idx = 0; idx < 16; ++idx) {
+        if (idx < 8) nxt[idx] = ks == 0 ? read_op(sb, 1, idx) : read_op(sn, 0, idx);
+        if (ks == 1 && idx % 2 == 0) load_one(idx / 2, min(s + HRING, nst - 1), lds0 + sb * HSTAGE);
+        const int nb = idx >> 2, mb = idx & 3;
+        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[4 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int r = 0; r < 8; ++r) cur[r] = nxt[r];
+    }
+  };
+  int s = 0;
+  for (; s + HRING <= nst; s += HRING) {
+    stage(std::integral_constant<int, 0>{}, s);
+    stage(std::integral_constant<int, 1>{}, s + 1);
+    stage(std::integral_constant<int, 2>{}, s + 2);
+    stage(std::integral_constant<int, 3>{}, s + 3);
+    stage(std::integral_constant<int, 4>{}, s + 4);
+  }
+  if (s < nst) stage(std::integral_constant<int, 0>{}, s);
+  if (s + 1 < nst) stage(std::integral_constant<int, 1>{}, s + 1);
+  if (s + 2 < nst) stage(std::integral_constant<int, 2>{}, s + 2);
+  if (s + 3 < nst) stage(std::integral_constant<int, 3>{}, s + 3);
+  // every wave drains its loads before the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+
+  // epilogue: lane holds m = m-block base + lr; n = n-block base + 8u + 4g + (0..3).
+  // The column scales and bias of the lane's 16 n-groups are loaded once.
+  f32x4 bsv[4][4];
+  i32x2 biv[4][4];
+  if constexpr (!RAW) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
+        if (ga.vec_ok && n + 3 < ga.n) {
+          bsv[i][u] = *(const f32x4 *)(ga.bs + n);
+          biv[i][u] = ga.bias ? *(const i32x2 *)(ga.bias + n) : i32x2{0, 0};
+        } else {
+          uint16_t bb[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int nn = min(n + e, ga.n - 1);
+            bsv[i][u][e] = ga.bs[nn];
+            bb[e] = ga.bias ? ga.bias[nn] : 0;
+          }
+          biv[i][u] = i32x2{(int)((uint32_t)bb[0] | ((uint32_t)bb[1] << 16)), (int)((uint32_t)bb[2] | ((uint32_t)bb[3] << 16))};
+        }
+      }
+  }
+  if constexpr (!RAW) {
+    if (ga.st_ok) {
+      // bf16 tile through LDS: each wave stages its 128 x 128 outputs in rows
+      // of 256 + 16 bytes, then writes 16 bytes per lane, 256-byte row segments
+      constexpr int ROWB = 128 * 2 + 16;
+      static_assert(HWAVES * 128 * ROWB <= HRING * HSTAGE, "staging fits the ring");
+      __syncthreads();  // every wave is done with the ring
+      const uint32_t wt = (uint32_t)(w * 128 * ROWB);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int m = m0 + wm * 128 + j * 32 + lr;
+        const float asm_ = ga.as[min(m, ga.m - 1)];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            uint16_t vals[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float t = (float)acc[i][j][4 * u + e];
+              t = t * bsv[i][u][e];
+              t = t * asm_;
+              if (ga.bias) {
+                const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
+                t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
+              }
+              vals[e] = f32_to_bf16_bits(t);
+            }
+            *(i32x2 *)(smem + wt + (j * 32 + lr) * ROWB + (i * 32 + 8 * u + 4 * g) * 2) =
+                i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                      (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+          }
+      }
+#pragma unroll
+      for (int it = 0; it < 32; ++it) {
+        const int r = it * 4 + (lane >> 4), c = lane & 15;
+        const i32x4 v = *(const i32x4 *)(smem + wt + r * ROWB + c * 16);
+        const int m = m0 + wm * 128 + r, n = n0 + wn * 128 + c * 8;
+        if (m < ga.m && n < ga.n) {
+          uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+          if (n + 7 < ga.n) {
+            *(i32x4 *)op = v;
+          } else {
+            for (int e = 0; e < 8 && n + e < ga.n; ++e) op[e] = (uint16_t)((uint32_t)v[e >> 1] >> (16 * (e & 1)));
+          }
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int m = m0 + wm * 128 + j * 32 + lr;
+    if (m >= ga.m) continue;
+    const float asm_ = RAW ? 0.0f : ga.as[m];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
+        if (n >= ga.n) continue;
+        if constexpr (RAW) {
+          int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
+          if (n + 3 < ga.n) {
+            *(i32x4 *)op = i32x4{acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
+          } else {
+            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[i][j][4 * u + e];
+          }
+        } else {
+          uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+          uint16_t vals[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float t = (float)acc[i][j][4 * u + e];
+            t = t * bsv[i][u][e];
+            t = t * asm_;
+            if (ga.bias) {
+              const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
+              t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
+            }
+            vals[e] = f32_to_bf16_bits(t);
+          }
+          if (n + 3 < ga.n) {
+            *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                                 (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+          } else {
+            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
+          }
+        }
+      }
+    }
+  }
+}
+
 template <bool RAW>
 int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, const float *bs, const void *bias,
                 int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *stream) {
@@ -306,9 +568,18 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
   if (((uintptr_t)a % 16) || ((uintptr_t)b % 16) || lda % 16 || ldb % 16 || lda < k || ldb < k || ldo < n)
     return set_error(TMHD_ERR_INVALID, "%s: operands must be 16-byte aligned rows with stride >= k", what);
   if (m == 0) return TMHD_OK;
-  GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + GBM - 1) / GBM, (n + GBN - 1) / GBN};
+  GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + GBM - 1) / GBM, (n + GBN - 1) / GBN,
+           (int32_t)(((uintptr_t)bs % 16) == 0 && ((uintptr_t)bias % 8) == 0),
+           (int32_t)(!RAW && ((uintptr_t)out % 16) == 0 && ldo % 8 == 0)};
   const int64_t grid = (int64_t)ga.tm_count * ga.tn_count;
-  hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(GWAVES * 64), 0, (hipStream_t)stream, ga);
+  // the one-wave-per-SIMD kernel takes 32-bit row offsets
+  const bool wide = (int64_t)(m - 1) * lda + k < ((int64_t)1 << 32) &&
+                    (int64_t)(n - 1) * ldb + k < ((int64_t)1 << 32);
+  if (wide)
+    hipLaunchKernelGGL(gemm_i8_wave128_kernel<RAW>, dim3((unsigned)grid), dim3(HWAVES * 64), 0, (hipStream_t)stream,
+                       ga);
+  else
+    hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(GWAVES * 64), 0, (hipStream_t)stream, ga);
   return check_launch(what);
 }
 
