@@ -850,7 +850,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     nv3 = tile_valid(sk);
   }
 
-  // ---- epilogue: O = O^T / l, written token-major (4 consecutive d per store)
+  // ---- epilogue: O = O^T / l, written token-major (4 consecutive d per store).
+  // The last iteration's tile loads (into buffers nobody reads) land before the
+  // workgroup's LDS is released.
+  wait_vmem();
   mfma_drain();
 #pragma unroll
   for (int hf = 0; hf < 2; ++hf)
