@@ -11,7 +11,7 @@ The same step with the INT8-QK backend and the W8A8 projection
 (12,252 x 5,120 -> 13,824, per-token INT8 X, per-channel INT8 W, bf16 bias)
 are measured beside it and reported in the same JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|bf16|i8qk|w8a8] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|bf16|i8qk|w8a8|rope] [--no-cpu-baseline]
 """
 
 from __future__ import annotations
@@ -171,6 +171,22 @@ def bench_w8a8(torch, dev, steps, warmup):
     return wall_ms, dev_ms, comps
 
 
+def bench_rope(torch, dev, steps, warmup):
+    """Q/K RMSNorm + RoPE in place in the merged QKV projection of the 768p chunk
+    (the step in front of the hook), synthetic bf16 inputs; returns ms per call."""
+    from taomate_hd_amd import fused_qkv_qk_norm_rope_
+
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qkv = _randn(torch, (LQ, 3 * H * D), gen, dev).to(torch.bfloat16)
+    qw = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
+    kw = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
+    ang = _randn(torch, (4096, D // 2), gen, dev)
+    cache = torch.cat([ang.cos(), ang.sin()], -1).to(torch.bfloat16)
+    pos = torch.arange(LQ, device=dev) % 4096
+    _, dev_ms = time_steps(torch, lambda: fused_qkv_qk_norm_rope_(qkv, qw, kw, cache, pos, 1e-6), steps, warmup)
+    return dev_ms
+
+
 def cpu_baseline(torch):
     """The reference serial backend (torch SDPA, fp32) on the host cores over the 768p attention.
 
@@ -221,7 +237,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "copy"), default="all")
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "copy"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -347,6 +363,19 @@ def main() -> int:
         if result["value"] is None:
             result["value"], result["ms_per_step"] = result["w8a8"]["gemm_tops"], round(wall_ms, 4)
             result["unit"] = "TOPS"
+    if args.workload in ("all", "rope"):
+        rope_ms = bench_rope(torch, dev, args.steps, args.warmup)
+        rbytes = 2.0 * 2.0 * LQ * H * D * 2  # Q and K read and written once
+        result["qkv_norm_rope"] = {
+            "us_per_call": round(rope_ms * 1e3, 1),
+            "gbps": round(rbytes / (rope_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(rbytes / (rope_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "shape": f"tokens {LQ}, heads {H}, head_dim {D}, rotary {D}, merged QKV in place",
+        }
+        _log(f"qkv norm+rope: {rope_ms * 1e3:.1f} us per call")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["qkv_norm_rope"]["gbps"], round(rope_ms, 4)
+            result["unit"] = "GB/s"
     if not args.no_cpu_baseline and args.workload in ("all", "bf16"):
         result["cpu_baseline"] = cpu_baseline(torch)
         _log(f"cpu baseline: {result['cpu_baseline']}")

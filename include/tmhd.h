@@ -162,6 +162,29 @@ int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride,
                  int32_t zero_to, int32_t heads, int32_t head_dim, void *stream);
 
 /*
+ * Q/K RMSNorm + RoPE in place inside a merged bf16 QKV projection
+ * qkv[tokens][row_stride] (Q, K, V of `heads` heads each, head_dim channels;
+ * V is neither read nor written).  Per token and head, with x the Q (or K)
+ * channels and w q_weight (or k_weight):
+ *   n = bf16((x * (1 / sqrt(sum(x^2) / head_dim + eps))) * w)
+ *   channel d < rotary_dim: bf16(bf16(n[d] * cos) + bf16(r[d] * sin)), where
+ *   r[d] = -n[d + h] (d < h) or n[d - h] (d >= h), h = rotary_dim / 2, and
+ *   cos / sin = cos_sin[p][d % h] / cos_sin[p][h + d % h] at p = positions[t]
+ *   (clamped to [0, cos_sin_rows)); other channels keep n.
+ * bf16() is round-to-nearest-even on the fp32 bits; the sum of squares runs
+ * per 8 channels in order, then as a butterfly over those partials; the
+ * square root and division are correctly rounded.
+ * Replaces fused_qkv_qk_norm_rope_ / _merged_qkv_preprocess_kernel,
+ * src/taomate_hd/inference/fused_kernels.py:425-472, 826-873.
+ * head_dim 64 or 128; rotary_dim a multiple of 16 up to head_dim.
+ */
+int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim,
+                       int64_t row_stride, const void *q_weight, const void *k_weight,
+                       const void *cos_sin, int64_t cos_sin_stride, int64_t cos_sin_rows,
+                       int32_t rotary_dim, const int64_t *positions, float eps,
+                       void *stream);
+
+/*
  * Per-token dynamic symmetric INT8 quantization of a bf16 [rows][cols]
  * matrix (row stride x_stride elements): scale[m] = amax_m / 127,
  * q[m][k] = sat_int8(rint(x[m][k] * (127 / amax_m))), amax_m = 0 -> 0.

@@ -1,0 +1,59 @@
+"""Q/K RMSNorm + RoPE inside the merged QKV projection, in front of the hook.
+
+``fused_qkv_qk_norm_rope_`` has the reference's signature, checks and error
+messages (src/taomate_hd/inference/fused_kernels.py:826-873) and runs the
+gfx950 kernel behind ``tmhd_qkv_norm_rope`` in place on the current stream.
+The arithmetic and bf16 rounding follow the reference's Triton kernel
+(``:425-472``); the order of the sum of squares and a correctly rounded
+inverse square root are fixed where the reference leaves them to its
+compiler (stated in include/tmhd.h).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+from . import _native
+
+
+def fused_qkv_qk_norm_rope_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any, positions: Any, eps: float) -> Any:
+    """Normalize and rotate Q/K in place in a merged bf16 QKV projection.
+
+    ``qkv`` is ``[tokens, 3 * heads * head_dim]`` (Q, K, V); V is not read or
+    written.  ``cos_sin_cache`` is ``[positions, rotary_dim]`` bf16 (cos in the
+    first half of a row, sin in the second) and ``positions`` holds one
+    position per token.  Returns ``qkv``.
+    """
+    import torch
+
+    if qkv.ndim != 2 or not qkv.is_contiguous():
+        raise ValueError("fused QKV preprocessing requires contiguous [tokens, width]")
+    if q_weight.shape != k_weight.shape or q_weight.ndim != 1:
+        raise ValueError("fused QKV Q/K norm weights differ")
+    if any(value.dtype != torch.bfloat16 for value in (qkv, q_weight, k_weight, cos_sin_cache)):
+        raise ValueError("fused QKV preprocessing requires BF16 tensors")
+    tokens = int(qkv.shape[0])
+    head_dim = int(q_weight.numel())
+    projection_width, remainder = divmod(int(qkv.shape[-1]), 3)
+    heads, head_remainder = divmod(projection_width, head_dim)
+    if remainder or head_remainder:
+        raise ValueError("fused QKV width does not contain three complete projections")
+    positions = positions.reshape(-1).to(device=qkv.device, dtype=torch.int64).contiguous()
+    if int(positions.numel()) != tokens:
+        raise ValueError("fused QKV RoPE positions do not cover every token")
+    cache = cos_sin_cache.contiguous()
+    rotary_dim = int(cache.shape[-1])
+    if cache.ndim != 2 or rotary_dim > head_dim or rotary_dim % 2:
+        raise ValueError("fused QKV RoPE cache span is invalid")
+    for name, t in (("qkv", qkv), ("q_weight", q_weight), ("k_weight", k_weight), ("cos_sin_cache", cache)):
+        if t.device != qkv.device or t.device.type != "cuda":
+            raise ValueError(f"{name} must be on the GPU of qkv")
+    q_weight = q_weight.contiguous()
+    k_weight = k_weight.contiguous()
+    status = _native.load().tmhd_qkv_norm_rope(
+        _native.ptr(qkv), tokens, heads, head_dim, qkv.stride(0), _native.ptr(q_weight), _native.ptr(k_weight),
+        _native.ptr(cache), cache.stride(0), int(cache.shape[0]), rotary_dim, _native.ptr(positions), float(eps),
+        _native.stream_ptr(torch, qkv.device),
+    )
+    _native.check(status, "tmhd_qkv_norm_rope")
+    return qkv

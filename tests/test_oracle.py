@@ -283,3 +283,88 @@ def test_hook_oracle_visibility_hand_derived():
     h.deactivate()
     with pytest.raises(RuntimeError):
         h("a", q, k, v, tags, mask, bounds, 0.5)
+
+
+# ---------------------------------------------------------------- QK norm + RoPE
+from oracle import rope as orope  # noqa: E402
+
+
+def test_round_bf16_bit_trick_matches_rne_and_edges():
+    # finite values: the integer formula is round-to-nearest-even (independent implementation in oracle.bf16)
+    x = np.random.default_rng(1).standard_normal(200000).astype(np.float32) * np.float32(3e4)
+    assert np.array_equal(orope.round_bf16(x).view(np.uint32), bf16.round_f32(x).view(np.uint32))
+    pats = np.array([0x3F808000, 0x3F818000, 0x7F7FFFFF, 0xFFFFFFFF, 0x7F800000, 0x80000000], np.uint32)
+    got = orope.round_bf16(pats.view(np.float32)).view(np.uint32)
+    # ties to even, overflow to inf, the all-ones NaN pattern wraps to +0 (as the fp32 add does), inf and -0 kept
+    assert list(got) == [0x3F800000, 0x3F820000, 0x7F800000, 0x00000000, 0x7F800000, 0x80000000]
+
+
+def test_sum_squares_order_against_float64():
+    x = np.random.default_rng(2).standard_normal((50, 128)).astype(np.float32)
+    got = orope.sum_squares(x).astype(np.float64)
+    want = (x.astype(np.float64) ** 2).sum(-1)
+    assert np.all(np.abs(got - want) <= 1e-5 * want)
+    # hand-derived order: partials over 8 channels, then the butterfly
+    # 2^24 first, then ones: inside the first chunk each + 1 rounds back to 2^24
+    # (ties to even); the second chunk's 8 ones survive as one partial.  Any
+    # other order (e.g. the ones first: 2^24 + 15 -> 2^24 + 16) gives another value.
+    y = np.ones((1, 16), np.float32)
+    y[0, 0] = 2.0 ** 12
+    assert orope.sum_squares(y)[0] == np.float32(2.0 ** 24 + 8.0)
+    assert np.float32(2.0 ** 24) + np.float32(15.0) != np.float32(2.0 ** 24 + 8.0)
+
+
+def _rope_case(tokens=7, heads=3, head_dim=128, rotary=128, seed=5):
+    rng = np.random.default_rng(seed)
+    qkv = bf16.round_f32(rng.standard_normal((tokens, 3 * heads * head_dim)).astype(np.float32) * 2)
+    qw = bf16.round_f32(1.0 + 0.1 * rng.standard_normal(head_dim).astype(np.float32))
+    kw = bf16.round_f32(1.0 + 0.1 * rng.standard_normal(head_dim).astype(np.float32))
+    half = rotary // 2
+    ang = rng.uniform(0, 6.3, (11, half))
+    cache = bf16.round_f32(np.concatenate([np.cos(ang), np.sin(ang)], -1).astype(np.float32))
+    pos = rng.integers(0, 11, tokens)
+    return qkv, qw, kw, cache, pos
+
+
+def test_qkv_norm_rope_closed_forms():
+    qkv, qw, kw, cache, pos = _rope_case()
+    T, H, D, R = 7, 3, 128, 128
+    out = orope.qkv_norm_rope(qkv, qw, kw, cache, pos, 1e-6, H)
+    # V untouched
+    assert np.array_equal(out[:, 2 * H * D:], qkv[:, 2 * H * D:])
+    # identity rotation (cos = 1, sin = 0): plain RMSNorm, within one bf16 ulp of the float64 formula
+    ident = np.concatenate([np.ones((11, R // 2)), np.zeros((11, R // 2))], -1).astype(np.float32)
+    nrm = orope.qkv_norm_rope(qkv, qw, kw, ident, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
+    x = qkv[:, : 2 * H * D].reshape(T, 2, H, D).astype(np.float64)
+    w = np.stack([qw, kw]).astype(np.float64)[None, :, None, :]
+    ref = x / np.sqrt((x * x).mean(-1, keepdims=True) + 1e-6) * w
+    assert np.all(np.abs(nrm - ref) <= 2.0 ** -7 * np.abs(ref) + 1e-30)
+    # rotate-half in float64: out[d] = n[d] cos - n[d+h] sin (d < h), n[d] cos + n[d-h] sin (d >= h)
+    h = R // 2
+    rows = cache[pos].astype(np.float64)
+    c = np.concatenate([rows[:, :h], rows[:, :h]], -1)[:, None, None, :]
+    s = np.concatenate([rows[:, h:], rows[:, h:]], -1)[:, None, None, :]
+    rot = np.concatenate([-nrm[..., h:], nrm[..., :h]], -1).astype(np.float64)
+    want = nrm.astype(np.float64) * c + rot * s
+    got = out[:, : 2 * H * D].reshape(T, 2, H, D)
+    assert np.all(np.abs(got - want) <= 2.0 ** -6 * (np.abs(nrm) + np.abs(rot)) * 1.0 + 1e-30)
+    # a rotation keeps the norm of each (d, d + h) pair
+    n2 = nrm[..., :h].astype(np.float64) ** 2 + nrm[..., h:].astype(np.float64) ** 2
+    g2 = got[..., :h].astype(np.float64) ** 2 + got[..., h:].astype(np.float64) ** 2
+    assert np.allclose(g2, n2, rtol=3e-2, atol=1e-6)
+
+
+def test_qkv_norm_rope_partial_rotary_and_weights_select_q_k():
+    qkv, qw, kw, cache, pos = _rope_case(rotary=64)
+    T, H, D, R = 7, 3, 128, 64
+    out = orope.qkv_norm_rope(qkv, qw, kw, cache, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
+    ident = np.concatenate([np.ones((11, R // 2)), np.zeros((11, R // 2))], -1).astype(np.float32)
+    nrm = orope.qkv_norm_rope(qkv, qw, kw, ident, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
+    # channels past the rotary span are only normalized
+    assert np.array_equal(out[..., R:], nrm[..., R:])
+    # Q uses q_weight and K uses k_weight: swapping the weights swaps nothing else
+    sw = orope.qkv_norm_rope(qkv, kw, qw, ident, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
+    x = qkv[:, : 2 * H * D].reshape(T, 2, H, D)
+    inv = np.float32(1) / np.sqrt(orope.sum_squares(x) / np.float32(D) + np.float32(1e-6))
+    assert np.array_equal(sw[:, 0], orope.round_bf16((x[:, 0] * inv[:, 0, :, None]) * kw))
+    assert np.array_equal(nrm[:, 1], orope.round_bf16((x[:, 1] * inv[:, 1, :, None]) * kw))
