@@ -18,9 +18,14 @@ phase d % (rotary_dim / 2)).
 
 Two things the reference leaves to its compiler are fixed here and in the
 HIP kernel:
-  * the order of the sum of squares: partial sums over 8 consecutive
-    channels (in channel order), then a butterfly over the partials
-    (partner index i ^ k for k = n/2, ..., 1);
+  * the order of the sum of squares.  A row's head_dim channels are dealt to
+    head_dim / 8 lanes of 8 channels each (lane_channels): lane j < rotary / 8
+    holds the 4 channels at 4j and the 4 at rotary / 2 + 4j (a rotation pair
+    per position), the remaining lanes hold 8 consecutive channels of the
+    unrotated tail.  Each lane sums the squares of its channels in that order
+    as a chain of fused multiply-adds (x0 * x0, then s + x * x rounded once),
+    and the lane partials are added as a balanced pairwise tree in lane order
+    ((l0 + l1) + (l2 + l3)) + ...;
   * the inverse RMS: 1 / sqrt(variance + eps) with a correctly rounded
     square root and division (the reference's tl.rsqrt is the GPU's
     approximate reciprocal square root).
@@ -41,19 +46,34 @@ def round_bf16(x: np.ndarray) -> np.ndarray:
     return (u & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
 
 
-def sum_squares(x: np.ndarray) -> np.ndarray:
-    """Sum of squares over the last axis (a multiple of 8) in the fixed order."""
+def lane_channels(head_dim: int, rotary: int) -> np.ndarray:
+    """[head_dim / 8, 8] channel indices of each lane of a row, in summation order."""
+    half = rotary // 2
+    lanes = []
+    for j in range(head_dim // 8):
+        if j < rotary // 8:
+            lanes.append([4 * j + e for e in range(4)] + [half + 4 * j + e for e in range(4)])
+        else:
+            base = rotary + 8 * (j - rotary // 8)
+            lanes.append(list(range(base, base + 8)))
+    return np.array(lanes, dtype=np.int64)
+
+
+def sum_squares(x: np.ndarray, rotary: int = 0) -> np.ndarray:
+    """Sum of squares over the last axis (head_dim, a multiple of 8) in the
+    fixed order for a row with the given rotary span."""
     x = np.asarray(x, dtype=np.float32)
-    n = x.shape[-1] // 8
-    chunks = x.reshape(*x.shape[:-1], n, 8)
+    chunks = x[..., lane_channels(x.shape[-1], rotary)]  # [..., lanes, 8]
     part = chunks[..., 0] * chunks[..., 0]
     for e in range(1, 8):
-        part = part + chunks[..., e] * chunks[..., e]
-    k = n // 2
-    idx = np.arange(n)
-    while k >= 1:
-        part = part + part[..., idx ^ k]
-        k //= 2
+        # fused multiply-add: x * x of a bf16 value is exact in float64 and the
+        # float64 sum of it and a float32 partial rounds to float32 as one
+        # rounding of the exact sum would (double rounding through a format
+        # of 53 >= 2 * 24 + 2 bits is innocuous for addition)
+        c = chunks[..., e].astype(np.float64)
+        part = (part.astype(np.float64) + c * c).astype(np.float32)
+    while part.shape[-1] > 1:
+        part = part[..., 0::2] + part[..., 1::2]
     return part[..., 0]
 
 
@@ -68,7 +88,7 @@ def qkv_norm_rope(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, c
     half = rotary // 2
     out = qkv.copy()
     x = qkv[:, : 2 * heads * head_dim].reshape(tokens, 2, heads, head_dim)
-    variance = sum_squares(x) / np.float32(head_dim)
+    variance = sum_squares(x, rotary) / np.float32(head_dim)
     inv = np.float32(1.0) / np.sqrt(variance + np.float32(eps))
     w = np.stack([np.asarray(q_weight, np.float32), np.asarray(k_weight, np.float32)])[None, :, None, :]
     normalized = round_bf16((x * inv[..., None]) * w)

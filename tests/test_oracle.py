@@ -299,19 +299,39 @@ def test_round_bf16_bit_trick_matches_rne_and_edges():
     assert list(got) == [0x3F800000, 0x3F820000, 0x7F800000, 0x00000000, 0x7F800000, 0x80000000]
 
 
+def test_lane_channels_partition_the_row_and_pair_rotations():
+    for d, r in [(128, 128), (128, 64), (128, 0), (64, 64), (64, 32), (64, 16)]:
+        ch = orope.lane_channels(d, r)
+        assert ch.shape == (d // 8, 8) and sorted(ch.ravel()) == list(range(d))
+        for j in range(r // 8):  # each rotary lane holds (d, d + r/2) pairs at the same places
+            assert list(ch[j, 4:] - ch[j, :4]) == [r // 2] * 4 and ch[j, 3] < r // 2
+
+
 def test_sum_squares_order_against_float64():
     x = np.random.default_rng(2).standard_normal((50, 128)).astype(np.float32)
-    got = orope.sum_squares(x).astype(np.float64)
-    want = (x.astype(np.float64) ** 2).sum(-1)
-    assert np.all(np.abs(got - want) <= 1e-5 * want)
-    # hand-derived order: partials over 8 channels, then the butterfly
-    # 2^24 first, then ones: inside the first chunk each + 1 rounds back to 2^24
-    # (ties to even); the second chunk's 8 ones survive as one partial.  Any
-    # other order (e.g. the ones first: 2^24 + 15 -> 2^24 + 16) gives another value.
+    for r in (0, 64, 128):
+        got = orope.sum_squares(x, r).astype(np.float64)
+        want = (x.astype(np.float64) ** 2).sum(-1)
+        assert np.all(np.abs(got - want) <= 1e-5 * want)
+    # hand-derived order, head_dim 16 rotary 16: lane 0 holds channels 0-3 and
+    # 8-11, lane 1 holds 4-7 and 12-15.  With 2^12 at channel 4, lane 1 starts
+    # at 2^24 and each + 1 after it rounds back (ties to even); lane 0 sums
+    # 8 ones; total 2^24 + 8.  Contiguous chunks of 8 would give
+    # (1 + 1 + 1 + 1 + 2^24 ...) + 8 = 2^24 + 12, the ones first 2^24 + 16.
     y = np.ones((1, 16), np.float32)
-    y[0, 0] = 2.0 ** 12
-    assert orope.sum_squares(y)[0] == np.float32(2.0 ** 24 + 8.0)
-    assert np.float32(2.0 ** 24) + np.float32(15.0) != np.float32(2.0 ** 24 + 8.0)
+    y[0, 4] = 2.0 ** 12
+    assert orope.sum_squares(y, 16)[0] == np.float32(2.0 ** 24 + 8.0)
+    assert orope.sum_squares(y, 0)[0] == np.float32(2.0 ** 24 + 12.0)
+    # fused multiply-add: with x0 = 2^-59, x1 = 2^-68 (1 + 2^-7), x1^2 =
+    # 2^-136 + 2^-142 + 2^-150 exactly.  2^-118 + x1^2 sits just above the
+    # midpoint between float32 neighbours 2^-141 apart, so one rounding gives
+    # 2^-118 + 2^-136 + 2^-141; a separate multiply would round x1^2 to
+    # 2^-136 + 2^-142 (a float32 subnormal) and the add would tie to even at
+    # 2^-118 + 2^-136.
+    z = np.zeros((1, 16), np.float32)
+    z[0, 0], z[0, 1] = 2.0 ** -59, 2.0 ** -68 * (1 + 2.0 ** -7)
+    assert orope.sum_squares(z, 16)[0] == np.float32(2.0 ** -118 + 2.0 ** -136 + 2.0 ** -141)
+    assert np.float32(z[0, 0] * z[0, 0]) + np.float32(z[0, 1] * z[0, 1]) == np.float32(2.0 ** -118 + 2.0 ** -136)
 
 
 def _rope_case(tokens=7, heads=3, head_dim=128, rotary=128, seed=5):
@@ -365,6 +385,6 @@ def test_qkv_norm_rope_partial_rotary_and_weights_select_q_k():
     # Q uses q_weight and K uses k_weight: swapping the weights swaps nothing else
     sw = orope.qkv_norm_rope(qkv, kw, qw, ident, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
     x = qkv[:, : 2 * H * D].reshape(T, 2, H, D)
-    inv = np.float32(1) / np.sqrt(orope.sum_squares(x) / np.float32(D) + np.float32(1e-6))
+    inv = np.float32(1) / np.sqrt(orope.sum_squares(x, R) / np.float32(D) + np.float32(1e-6))
     assert np.array_equal(sw[:, 0], orope.round_bf16((x[:, 0] * inv[:, 0, :, None]) * kw))
     assert np.array_equal(nrm[:, 1], orope.round_bf16((x[:, 1] * inv[:, 1, :, None]) * kw))
