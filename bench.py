@@ -35,6 +35,9 @@ PEAK_INT8_TOPS = 5033.2
 PEAK_HBM_GBPS = 8000.0
 
 H, D = 40, 128
+# rotary span of the DiT: cos / sin of 3 position axes x 16 frequencies, both halves
+# (model/architecture.py:31, model/layers.py:150-165)
+ROTARY = 96
 LQ = 12252  # 3 latent frames x 48 x 84 video tokens + 156 audio tokens
 VIDEO, AUDIO = 12096, 156
 ANCHOR = 4032
@@ -180,7 +183,7 @@ def bench_rope(torch, dev, steps, warmup):
     qkv = _randn(torch, (LQ, 3 * H * D), gen, dev).to(torch.bfloat16)
     qw = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
     kw = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
-    ang = _randn(torch, (4096, D // 2), gen, dev)
+    ang = _randn(torch, (4096, ROTARY // 2), gen, dev)
     cache = torch.cat([ang.cos(), ang.sin()], -1).to(torch.bfloat16)
     pos = torch.arange(LQ, device=dev) % 4096
     _, dev_ms = time_steps(torch, lambda: fused_qkv_qk_norm_rope_(qkv, qw, kw, cache, pos, 1e-6), steps, warmup)
@@ -370,7 +373,7 @@ def main() -> int:
             "us_per_call": round(rope_ms * 1e3, 1),
             "gbps": round(rbytes / (rope_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(rbytes / (rope_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-            "shape": f"tokens {LQ}, heads {H}, head_dim {D}, rotary {D}, merged QKV in place",
+            "shape": f"tokens {LQ}, heads {H}, head_dim {D}, rotary {ROTARY}, merged QKV in place",
         }
         _log(f"qkv norm+rope: {rope_ms * 1e3:.1f} us per call")
         if result["value"] is None:

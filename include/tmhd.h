@@ -171,18 +171,52 @@ int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride,
  *   r[d] = -n[d + h] (d < h) or n[d - h] (d >= h), h = rotary_dim / 2, and
  *   cos / sin = cos_sin[p][d % h] / cos_sin[p][h + d % h] at p = positions[t]
  *   (clamped to [0, cos_sin_rows)); other channels keep n.
- * bf16() is round-to-nearest-even on the fp32 bits; the sum of squares runs
- * per 8 channels in order, then as a butterfly over those partials; the
- * square root and division are correctly rounded.
+ * bf16() is round-to-nearest-even.  The sum of squares is fixed: the row's
+ * channels are dealt to head_dim / 8 partials of 8 (partial j < rotary_dim / 8
+ * takes channels 4j..4j+3 then h+4j..h+4j+3, the rest 8 consecutive channels
+ * of the tail), each a chain of fused multiply-adds, added as a pairwise tree
+ * in order.  The square root and division are correctly rounded.
  * Replaces fused_qkv_qk_norm_rope_ / _merged_qkv_preprocess_kernel,
- * src/taomate_hd/inference/fused_kernels.py:425-472, 826-873.
- * head_dim 64 or 128; rotary_dim a multiple of 16 up to head_dim.
+ * src/taomate_hd/inference/fused_kernels.py:425-472, 824-873.
+ * head_dim 64 or 128; rotary_dim a multiple of 8 up to head_dim; qkv rows,
+ * weights and cos_sin rows 8-byte aligned.
  */
 int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim,
                        int64_t row_stride, const void *q_weight, const void *k_weight,
                        const void *cos_sin, int64_t cos_sin_stride, int64_t cos_sin_rows,
                        int32_t rotary_dim, const int64_t *positions, float eps,
                        void *stream);
+
+/*
+ * The same RMSNorm + RoPE on one projection value[tokens][heads][head_dim]
+ * (row stride value_stride elements, heads * head_dim contiguous), written to
+ * out (row stride out_stride; out == value with equal strides is in place,
+ * any other overlap is refused), with one weight and per-token rotation
+ * tables: channel d < rotary_dim uses cos[t][d] and sin[t][d] (row strides
+ * cos_stride / sin_stride), r[d] as above.  Same fixed reduction order and
+ * rounding.
+ * Replaces fused_qk_norm_rope / _qk_norm_rope_kernel,
+ * src/taomate_hd/inference/fused_kernels.py:385-422, 798-821.
+ * head_dim 64 or 128; rotary_dim a multiple of 8 up to head_dim; rows 8-byte
+ * aligned.
+ */
+int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t head_dim,
+                      int64_t value_stride, void *out, int64_t out_stride,
+                      const void *weight, const void *cos, int64_t cos_stride,
+                      const void *sin, int64_t sin_stride, int32_t rotary_dim, float eps,
+                      void *stream);
+
+/*
+ * No counterpart in the reference: a device self-check for deployments and
+ * tests.  Runs every one of the 2^32 float bit patterns through the two
+ * rounding helpers the norm + RoPE kernels depend on and adds the failures
+ * to counts[0] (f32 -> bf16 conversion differing from the reference's
+ * integer rounding, fused_kernels.py:58-61, on any non-NaN value or quiet NaN
+ * with a zero low half) and counts[1] (square root not correctly rounded).
+ * counts: two device uint64 the caller has zeroed; both stay 0 on a sound
+ * device.  A few milliseconds on the stream.
+ */
+int tmhd_selfcheck_rounding(unsigned long long *counts, void *stream);
 
 /*
  * Per-token dynamic symmetric INT8 quantization of a bf16 [rows][cols]

@@ -1,20 +1,23 @@
-"""Q/K RMSNorm + RoPE inside a merged QKV projection (CPU restatement).
+"""Q/K RMSNorm + RoPE (CPU restatement).
 
 Test infrastructure only: tests and the bench's CPU baseline use it as the
 checker; the product path never imports it.
 
-Restates fused_qkv_qk_norm_rope_ / _merged_qkv_preprocess_kernel,
-src/taomate_hd/inference/fused_kernels.py:425-472 and 826-873, with the
-rounding helper _round_bf16 (:58-61).  For every token and head, Q and K
-(not V) of the [tokens, 3 * heads * head_dim] bf16 buffer become
+Restates fused_qkv_qk_norm_rope_ / _merged_qkv_preprocess_kernel
+(qkv_norm_rope) and fused_qk_norm_rope / _qk_norm_rope_kernel
+(qk_norm_rope), src/taomate_hd/inference/fused_kernels.py:385-472 and
+798-873, with the rounding helper _round_bf16 (:58-61).  For every token and
+head, Q and K (not V) of the [tokens, 3 * heads * head_dim] bf16 buffer (or
+one [tokens, heads, head_dim] projection) become
 
     normalized = bf16((x * rsqrt(mean(x^2) + eps)) * weight)
     rope       = bf16(bf16(normalized * cos) + bf16(rotate_half(normalized) * sin))
 
-for the first rotary_dim channels (normalized for the rest), with cos / sin
-read at the token's position from a bf16 [positions, rotary_dim] cache
-(cos in the first half of a row, sin in the second, channel d using
-phase d % (rotary_dim / 2)).
+for the first rotary_dim channels (normalized for the rest).  The merged form
+reads cos / sin at the token's position from a bf16 [positions, rotary_dim]
+cache (cos in the first half of a row, sin in the second, channel d using
+phase d % (rotary_dim / 2)); the one-projection form reads per-token,
+per-channel tables cos[t][d], sin[t][d].
 
 Two things the reference leaves to its compiler are fixed here and in the
 HIP kernel:
@@ -77,10 +80,31 @@ def sum_squares(x: np.ndarray, rotary: int = 0) -> np.ndarray:
     return part[..., 0]
 
 
+def _norm_rope(x: np.ndarray, w: np.ndarray, cos_d: np.ndarray, sin_d: np.ndarray, rotary: int,
+               eps: float) -> np.ndarray:
+    """x [..., head_dim] (bf16 values as float32), w broadcastable to it,
+    cos_d / sin_d broadcastable to [..., rotary] (channel d's cos and sin)."""
+    head_dim = x.shape[-1]
+    half = rotary // 2
+    variance = sum_squares(x, rotary) / np.float32(head_dim)
+    inv = np.float32(1.0) / np.sqrt(variance + np.float32(eps))
+    normalized = round_bf16((x * inv[..., None]) * w)
+    if rotary:
+        d = np.arange(rotary)
+        paired = normalized[..., np.where(d < half, d + half, d - half)]
+        rotated = np.where(d < half, -paired, paired)
+        cos = round_bf16(np.asarray(cos_d, dtype=np.float32))
+        sin = round_bf16(np.asarray(sin_d, dtype=np.float32))
+        rope = round_bf16(round_bf16(normalized[..., :rotary] * cos) + round_bf16(rotated * sin))
+        normalized = np.concatenate([rope, normalized[..., rotary:]], -1)
+    return normalized
+
+
 def qkv_norm_rope(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, cos_sin: np.ndarray,
                   positions: np.ndarray, eps: float, heads: int) -> np.ndarray:
     """Q/K of a merged [tokens, 3 * heads * head_dim] buffer (bf16 values as
-    float32) normalized and rotated; V unchanged.  Returns a new array."""
+    float32) normalized and rotated; V unchanged.  Returns a new array.
+    fused_kernels.py:425-472, 824-873."""
     qkv = np.asarray(qkv, dtype=np.float32)
     tokens, width = qkv.shape
     head_dim = width // (3 * heads)
@@ -88,21 +112,25 @@ def qkv_norm_rope(qkv: np.ndarray, q_weight: np.ndarray, k_weight: np.ndarray, c
     half = rotary // 2
     out = qkv.copy()
     x = qkv[:, : 2 * heads * head_dim].reshape(tokens, 2, heads, head_dim)
-    variance = sum_squares(x, rotary) / np.float32(head_dim)
-    inv = np.float32(1.0) / np.sqrt(variance + np.float32(eps))
     w = np.stack([np.asarray(q_weight, np.float32), np.asarray(k_weight, np.float32)])[None, :, None, :]
-    normalized = round_bf16((x * inv[..., None]) * w)
-    d = np.arange(head_dim)
-    rot = d < rotary
+    cos_d = sin_d = None
     if rotary:
-        partner = np.where(d < half, d + half, d - half)
-        paired = normalized[..., np.where(rot, partner, d)]
-        rotated = np.where(d < half, -paired, paired)
-        phase = d % half
+        phase = np.arange(rotary) % half
         rows = np.asarray(cos_sin, dtype=np.float32)[np.asarray(positions, dtype=np.int64)]  # [tokens, rotary]
-        cos = round_bf16(rows[:, np.where(rot, phase, 0)])[:, None, None, :]
-        sin = round_bf16(rows[:, np.where(rot, half + phase, 0)])[:, None, None, :]
-        rope = round_bf16(round_bf16(normalized * cos) + round_bf16(rotated * sin))
-        normalized = np.where(rot, rope, normalized)
+        cos_d = rows[:, phase][:, None, None, :]
+        sin_d = rows[:, half + phase][:, None, None, :]
+    normalized = _norm_rope(x, w, cos_d, sin_d, rotary, eps)
     out[:, : 2 * heads * head_dim] = normalized.reshape(tokens, 2 * heads * head_dim)
     return out
+
+
+def qk_norm_rope(value: np.ndarray, weight: np.ndarray, cos: np.ndarray, sin: np.ndarray,
+                 eps: float) -> np.ndarray:
+    """One projection [tokens, heads, head_dim] (bf16 values as float32)
+    normalized and rotated with per-token tables cos / sin [tokens, rotary].
+    fused_kernels.py:385-422, 798-821."""
+    value = np.asarray(value, dtype=np.float32)
+    rotary = int(np.asarray(cos).shape[-1])
+    cos_d = np.asarray(cos, np.float32)[:, None, :] if rotary else None
+    sin_d = np.asarray(sin, np.float32)[:, None, :] if rotary else None
+    return _norm_rope(value, np.asarray(weight, np.float32), cos_d, sin_d, rotary, eps)

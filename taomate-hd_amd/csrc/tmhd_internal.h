@@ -39,6 +39,38 @@ __host__ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Two floats -> packed bf16 (lo in bits 0-15) with gfx950's conversion,
+// round to nearest even.
+__device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
+  using f32x2_t = float __attribute__((ext_vector_type(2)));
+  const f32x2_t f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
+}
+
+// Correctly rounded square root of x >= 0 (+inf and NaN pass through).  The
+// hardware square root is within one ulp; the Tuckerman rounding test picks
+// between it and its two neighbours s- < s < s+: sqrt(x) lies below the
+// midpoint (s- + s) / 2 exactly when x - s- * s <= 0, and above (s + s+) / 2
+// exactly when x - s * s+ > 0.  Both residuals are whole multiples of the
+// squared spacing g^2 of the neighbours, while a midpoint's own residual is
+// g^2 / 4, so the signs decide; each residual is one fused multiply-add,
+// whose rounding keeps the sign.  Inputs below 2^-96 are scaled by 2^64 (and
+// the root by 2^-32, both exact) so that g^2 stays above the subnormal range.
+__device__ __forceinline__ float sqrt_rn(float x) {
+  const bool tiny = x < 0x1p-96f;
+  const float xs = tiny ? x * 0x1p64f : x;
+  float s = __builtin_amdgcn_sqrtf(xs);
+  if (s > 0.0f && s < __builtin_inff()) {
+    const float sd = __uint_as_float(__float_as_uint(s) - 1u);
+    const float su = __uint_as_float(__float_as_uint(s) + 1u);
+    if (__builtin_fmaf(-sd, s, xs) <= 0.0f)
+      s = sd;
+    else if (__builtin_fmaf(-s, su, xs) > 0.0f)
+      s = su;
+  }
+  return tiny ? s * 0x1p-32f : s;
+}
+
 // Slot position of token t inside the transposed value rows: swap the middle
 // two 4-token chunks of each 16-token group (an involution).
 __host__ __device__ __forceinline__ int vt_position(int t) {

@@ -19,7 +19,7 @@
 //     in lane order (DPP: lane ^ 1, ^ 2, mirror within 8, mirror within 16,
 //     which add the same pairs as the tree);
 //   * inverse RMS: 1 / sqrt(variance + eps) with correctly rounded square
-//     root and division.
+//     root (sqrt_rn) and division.
 // The bf16 rounding is gfx950's f32 -> bf16 conversion (round to nearest
 // even).  It gives the reference's integer rounding (+ 0x7FFF + bit 16, low
 // half cleared) for every non-NaN float and for every quiet NaN whose low 16
@@ -32,13 +32,7 @@
 namespace tmhd {
 namespace {
 
-using float2_t = float __attribute__((ext_vector_type(2)));
-
-// Two floats to packed bf16, rounded to nearest even; and back.
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  const float2_t f = {lo, hi};
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
-}
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return pack_bf16_rne(lo, hi); }
 __device__ __forceinline__ float lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
@@ -49,64 +43,80 @@ __device__ __forceinline__ float dpp(float x) {
 constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kHalfRowMirror = 0x141, kRowMirror = 0x140;
 
 struct RopeArgs {
-  uint16_t *qkv;
-  int64_t row_stride;  // elements between tokens
-  const uint16_t *qw, *kw;
-  const uint16_t *cs;  // cos | sin rows
-  int64_t cs_stride;
-  const int64_t *pos;
-  int64_t cs_rows;  // positions are clamped to [0, cs_rows)
-  int32_t tokens, heads, rotary;
+  const uint16_t *src;
+  uint16_t *dst;               // may equal src (in place)
+  int64_t src_stride, dst_stride;  // elements between tokens
+  const uint16_t *qw, *kw;     // kw for the rows of the second projection
+  const uint16_t *cos, *sin;   // TABLE: cos = the cos | sin cache, sin unused
+  int64_t cos_stride, sin_stride;
+  const int64_t *pos;          // TABLE only
+  int64_t cs_rows;             // TABLE only: positions are clamped to [0, cs_rows)
+  int32_t tokens, heads, parts, rotary;  // parts: 2 = Q then K of each token, 1 = one projection
   float eps;
 };
 
 constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad in the inverse RMS pass
 
-template <int D>
-__global__ void __launch_bounds__(256) qkv_norm_rope_kernel(const RopeArgs a) {
+// TABLE: cos / sin of channel d at cos_sin[positions[t]][d % h] and [h + d % h]
+// (the merged-projection form); otherwise at cos[t][d] and sin[t][d].
+template <int D, bool TABLE>
+__global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave and group
   constexpr int U = kRopeUnroll;
   const int lane = threadIdx.x & 63, j = lane % LPR;
-  const int two_h = 2 * a.heads;  // tokens * two_h is below 2^31 (host check)
+  const int per_token = a.parts * a.heads;  // tokens * per_token is below 2^31 (host check)
   const int row0 = (blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * U * RPW + lane / LPR;
   const int half = a.rotary >> 1, rot_lanes = a.rotary >> 3;
   const bool rotates = j < rot_lanes;
   const int oa = rotates ? 4 * j : a.rotary + 8 * (j - rot_lanes);  // channel of piece A
   const int ob = rotates ? half + 4 * j : oa + 4;                   // channel of piece B
-  uint16_t *ptr[U];
+  int64_t src_off[U], dst_off[U];
+  int tok[U];
   bool live[U], is_k[U];
   int64_t pos[U];
-  int token = row0 / two_h, rem = row0 - token * two_h;
+  int token = row0 / per_token, rem = row0 - token * per_token;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     if (u) {
       rem += RPW;
-      while (rem >= two_h) rem -= two_h, ++token;
+      while (rem >= per_token) rem -= per_token, ++token;
     }
     live[u] = token < a.tokens;
     const int t = live[u] ? token : a.tokens - 1;  // lanes past the end compute a copy of the last row, unstored
-    const int r = live[u] ? rem : two_h - 1;
+    const int r = live[u] ? rem : per_token - 1;
+    tok[u] = t;
     is_k[u] = r >= a.heads;
-    ptr[u] = a.qkv + (int64_t)t * a.row_stride + (int64_t)r * D;
-    if (a.rotary) pos[u] = a.pos[t];  // issued first: the cos / sin loads wait only for these
+    src_off[u] = (int64_t)t * a.src_stride + (int64_t)r * D;
+    dst_off[u] = (int64_t)t * a.dst_stride + (int64_t)r * D;
+    if (TABLE && a.rotary) pos[u] = a.pos[t];  // issued first: the cos / sin loads wait only for these
   }
-  i32x2 xa[U], xb[U], ca[U], sa[U];
+  i32x2 xa[U], xb[U], ca[U], sa[U], cb[U], sb[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    xa[u] = *(const i32x2 *)(ptr[u] + oa);
-    xb[u] = *(const i32x2 *)(ptr[u] + ob);
+    xa[u] = *(const i32x2 *)(a.src + src_off[u] + oa);
+    xb[u] = *(const i32x2 *)(a.src + src_off[u] + ob);
   }
   const i32x2 qwa = *(const i32x2 *)(a.qw + oa), qwb = *(const i32x2 *)(a.qw + ob);
   const i32x2 kwa = *(const i32x2 *)(a.kw + oa), kwb = *(const i32x2 *)(a.kw + ob);
   if (a.rotary) {
+    const int ph = rotates ? 4 * j : 0;  // lanes of the unrotated tail read a valid phase, unused
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t p = min(max(pos[u], (int64_t)0), a.cs_rows - 1);
-      const uint16_t *crow = a.cs + p * a.cs_stride + (rotates ? 4 * j : 0);
-      ca[u] = *(const i32x2 *)crow;
-      sa[u] = *(const i32x2 *)(crow + half);
+      if (TABLE) {
+        const int64_t p = min(max(pos[u], (int64_t)0), a.cs_rows - 1);
+        const uint16_t *crow = a.cos + p * a.cos_stride + ph;
+        ca[u] = *(const i32x2 *)crow;
+        sa[u] = *(const i32x2 *)(crow + half);
+      } else {
+        const uint16_t *crow = a.cos + (int64_t)tok[u] * a.cos_stride + ph;
+        const uint16_t *srow = a.sin + (int64_t)tok[u] * a.sin_stride + ph;
+        ca[u] = *(const i32x2 *)crow;
+        cb[u] = *(const i32x2 *)(crow + half);
+        sa[u] = *(const i32x2 *)srow;
+        sb[u] = *(const i32x2 *)(srow + half);
+      }
     }
   }
 
@@ -132,7 +142,7 @@ __global__ void __launch_bounds__(256) qkv_norm_rope_kernel(const RopeArgs a) {
   const int q = lane & 3;
   const float sq = q == 0 ? ss[0] : q == 1 ? ss[1] : q == 2 ? ss[2] : ss[3];
   const float var = sq * (1.0f / D);  // exact: D is a power of two
-  const float inv_q = __fdiv_rn(1.0f, __fsqrt_rn(var + a.eps));
+  const float inv_q = __fdiv_rn(1.0f, sqrt_rn(var + a.eps));
   const float inv[U] = {dpp<0x00>(inv_q), dpp<0x55>(inv_q), dpp<0xaa>(inv_q), dpp<0xff>(inv_q)};
 
   const uint32_t qw[4] = {(uint32_t)qwa[0], (uint32_t)qwa[1], (uint32_t)qwb[0], (uint32_t)qwb[1]};
@@ -147,19 +157,19 @@ __global__ void __launch_bounds__(256) qkv_norm_rope_kernel(const RopeArgs a) {
     }
     uint32_t out[4] = {nb[0], nb[1], nb[2], nb[3]};
     if (a.rotary) {
-      // rotation pairs (A[e], B[e]): A' = A cos - B sin, B' = B cos + A sin, each
-      // product and sum rounded to bf16 (rotate_half(n) = (-B, A))
-      const uint32_t cw[2] = {(uint32_t)ca[u][0], (uint32_t)ca[u][1]};
-      const uint32_t sw[2] = {(uint32_t)sa[u][0], (uint32_t)sa[u][1]};
+      // rotation pairs (A[e], B[e]): A' = A cos_A - B sin_A, B' = B cos_B + A sin_B,
+      // each product and sum rounded to bf16 (rotate_half(n) = (-B, A))
+      const uint32_t cwa[2] = {(uint32_t)ca[u][0], (uint32_t)ca[u][1]};
+      const uint32_t swa[2] = {(uint32_t)sa[u][0], (uint32_t)sa[u][1]};
+      const uint32_t cwb[2] = {(uint32_t)(TABLE ? ca : cb)[u][0], (uint32_t)(TABLE ? ca : cb)[u][1]};
+      const uint32_t swb[2] = {(uint32_t)(TABLE ? sa : sb)[u][0], (uint32_t)(TABLE ? sa : sb)[u][1]};
       float oa_[4], ob_[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float na = (e & 1) ? hi_f32(nb[e >> 1]) : lo_f32(nb[e >> 1]);
-        const float nbv = (e & 1) ? hi_f32(nb[2 + (e >> 1)]) : lo_f32(nb[2 + (e >> 1)]);
-        const float c = (e & 1) ? hi_f32(cw[e >> 1]) : lo_f32(cw[e >> 1]);
-        const float sn = (e & 1) ? hi_f32(sw[e >> 1]) : lo_f32(sw[e >> 1]);
-        const uint32_t p1 = pack_bf16(na * c, nbv * sn);  // A cos, B sin
-        const uint32_t p2 = pack_bf16(nbv * c, na * sn);  // B cos, A sin
+        const auto half_of = [e](uint32_t wd) { return (e & 1) ? hi_f32(wd) : lo_f32(wd); };
+        const float na = half_of(nb[e >> 1]), nbv = half_of(nb[2 + (e >> 1)]);
+        const uint32_t p1 = pack_bf16(na * half_of(cwa[e >> 1]), nbv * half_of(swa[e >> 1]));  // A cos, B sin
+        const uint32_t p2 = pack_bf16(nbv * half_of(cwb[e >> 1]), na * half_of(swb[e >> 1]));  // B cos, A sin
         oa_[e] = lo_f32(p1) - hi_f32(p1);
         ob_[e] = lo_f32(p2) + hi_f32(p2);
       }
@@ -171,11 +181,30 @@ __global__ void __launch_bounds__(256) qkv_norm_rope_kernel(const RopeArgs a) {
       }
     }
     if (live[u]) {
-      *(i32x2 *)(ptr[u] + oa) = i32x2{(int)out[0], (int)out[1]};
-      *(i32x2 *)(ptr[u] + ob) = i32x2{(int)out[2], (int)out[3]};
+      *(i32x2 *)(a.dst + dst_off[u] + oa) = i32x2{(int)out[0], (int)out[1]};
+      *(i32x2 *)(a.dst + dst_off[u] + ob) = i32x2{(int)out[2], (int)out[3]};
     }
   }
 }
+
+int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what) {
+  const int64_t rows = (int64_t)a.tokens * a.parts * a.heads;
+  const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
+  if (rows > 0x7fffffff - rows_per_block) return set_error(TMHD_ERR_UNSUPPORTED, "%s: too many rows", what);
+  const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 128 && table)
+    hipLaunchKernelGGL((qk_norm_rope_kernel<128, true>), grid, block, 0, s, a);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL((qk_norm_rope_kernel<128, false>), grid, block, 0, s, a);
+  else if (table)
+    hipLaunchKernelGGL((qk_norm_rope_kernel<64, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_kernel<64, false>), grid, block, 0, s, a);
+  return check_launch(what);
+}
+
+bool aligned8(const void *p) { return ((uintptr_t)p % 8) == 0; }
 
 }  // namespace
 }  // namespace tmhd
@@ -191,26 +220,54 @@ extern "C" int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int3
   if (tokens < 0 || heads <= 0 || row_stride < (int64_t)3 * heads * head_dim)
     return set_error(TMHD_ERR_INVALID, "%s: tokens %d heads %d row_stride %lld", what, tokens, heads,
                      (long long)row_stride);
-  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 16)
-    return set_error(TMHD_ERR_UNSUPPORTED, "%s: rotary_dim %d (a multiple of 16 up to head_dim)", what, rotary_dim);
+  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 8)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: rotary_dim %d (a multiple of 8 up to head_dim)", what, rotary_dim);
   if (!(eps >= 0.0f)) return set_error(TMHD_ERR_INVALID, "%s: eps must be >= 0", what);
   if (tokens == 0) return TMHD_OK;
-  if (!qkv || !q_weight || !k_weight || ((uintptr_t)qkv % 16) || row_stride % 8 || ((uintptr_t)q_weight % 16) ||
-      ((uintptr_t)k_weight % 16))
-    return set_error(TMHD_ERR_INVALID, "%s: qkv and weights must be 16-byte aligned rows", what);
-  if (rotary_dim && (!cos_sin || !positions || ((uintptr_t)cos_sin % 16) || cos_sin_stride % 8 ||
+  if (!qkv || !q_weight || !k_weight || !aligned8(qkv) || row_stride % 4 || !aligned8(q_weight) ||
+      !aligned8(k_weight))
+    return set_error(TMHD_ERR_INVALID, "%s: qkv rows and weights must be 8-byte aligned", what);
+  if (rotary_dim && (!cos_sin || !positions || !aligned8(cos_sin) || cos_sin_stride % 4 ||
                      cos_sin_stride < rotary_dim || cos_sin_rows <= 0))
-    return set_error(TMHD_ERR_INVALID, "%s: cos_sin must be 16-byte aligned rows of >= rotary_dim", what);
-  RopeArgs a{(uint16_t *)qkv, row_stride, (const uint16_t *)q_weight, (const uint16_t *)k_weight,
-             (const uint16_t *)cos_sin, cos_sin_stride, positions, cos_sin_rows, tokens, heads, rotary_dim, eps};
-  const int64_t rows = (int64_t)tokens * 2 * heads;
-  const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
-  const int64_t blocks = (rows + rows_per_block - 1) / rows_per_block;
-  if (rows > 0x7fffffff - rows_per_block) return set_error(TMHD_ERR_UNSUPPORTED, "%s: too many rows", what);
-  hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 128)
-    hipLaunchKernelGGL(qkv_norm_rope_kernel<128>, dim3((unsigned)blocks), dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL(qkv_norm_rope_kernel<64>, dim3((unsigned)blocks), dim3(256), 0, s, a);
-  return check_launch(what);
+    return set_error(TMHD_ERR_INVALID, "%s: cos_sin must be 8-byte aligned rows of >= rotary_dim", what);
+  RopeArgs a{(const uint16_t *)qkv, (uint16_t *)qkv, row_stride, row_stride, (const uint16_t *)q_weight,
+             (const uint16_t *)k_weight, (const uint16_t *)cos_sin, nullptr, cos_sin_stride, 0, positions,
+             cos_sin_rows, tokens, heads, 2, rotary_dim, eps};
+  return launch_rope(a, head_dim, true, stream, what);
+}
+
+extern "C" int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t head_dim,
+                                 int64_t value_stride, void *out, int64_t out_stride, const void *weight,
+                                 const void *cos, int64_t cos_stride, const void *sin, int64_t sin_stride,
+                                 int32_t rotary_dim, float eps, void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_qk_norm_rope";
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
+  if (tokens < 0 || heads <= 0 || value_stride < (int64_t)heads * head_dim || out_stride < (int64_t)heads * head_dim)
+    return set_error(TMHD_ERR_INVALID, "%s: tokens %d heads %d strides %lld / %lld", what, tokens, heads,
+                     (long long)value_stride, (long long)out_stride);
+  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 8)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: rotary_dim %d (a multiple of 8 up to head_dim)", what, rotary_dim);
+  if (!(eps >= 0.0f)) return set_error(TMHD_ERR_INVALID, "%s: eps must be >= 0", what);
+  if (tokens == 0) return TMHD_OK;
+  if (!value || !out || !weight || !aligned8(value) || !aligned8(out) || value_stride % 4 || out_stride % 4 ||
+      !aligned8(weight))
+    return set_error(TMHD_ERR_INVALID, "%s: value / out rows and the weight must be 8-byte aligned", what);
+  if (rotary_dim && (!cos || !sin || !aligned8(cos) || !aligned8(sin) || cos_stride % 4 || sin_stride % 4 ||
+                     cos_stride < rotary_dim || sin_stride < rotary_dim))
+    return set_error(TMHD_ERR_INVALID, "%s: cos / sin must be 8-byte aligned rows of >= rotary_dim", what);
+  if (out != value) {  // out-of-place: the two row sets must not overlap
+    const char *v0 = (const char *)value, *o0 = (const char *)out;
+    const int64_t vb = ((int64_t)(tokens - 1) * value_stride + (int64_t)heads * head_dim) * 2;
+    const int64_t ob = ((int64_t)(tokens - 1) * out_stride + (int64_t)heads * head_dim) * 2;
+    if (o0 < v0 + vb && v0 < o0 + ob)
+      return set_error(TMHD_ERR_INVALID, "%s: out overlaps value (only exact in-place is allowed)", what);
+  } else if (out_stride != value_stride) {
+    return set_error(TMHD_ERR_INVALID, "%s: in place needs equal strides", what);
+  }
+  RopeArgs a{(const uint16_t *)value, (uint16_t *)out, value_stride, out_stride, (const uint16_t *)weight,
+             (const uint16_t *)weight, (const uint16_t *)cos, (const uint16_t *)sin, cos_stride, sin_stride,
+             nullptr, 0, tokens, heads, 1, rotary_dim, eps};
+  return launch_rope(a, head_dim, false, stream, what);
 }

@@ -29,7 +29,7 @@ from .kvcache import (
     KVContract,
     kv_contract_from_model,
 )
-from .rope import fused_qkv_qk_norm_rope_
+from .rope import fused_qk_norm_rope, fused_qkv_qk_norm_rope_
 from .quant import (
     cutlass_scaled_mm,
     cutlass_scaled_mm_out,
@@ -51,6 +51,7 @@ from .w8a8 import (
 )
 
 __all__ = [
+    "fused_qk_norm_rope",
     "fused_qkv_qk_norm_rope_",
     "_native",
     "AVKV",

@@ -1,10 +1,12 @@
-"""Q/K RMSNorm + RoPE inside the merged QKV projection, in front of the hook.
+"""Q/K RMSNorm + RoPE in front of the hook.
 
-``fused_qkv_qk_norm_rope_`` has the reference's signature, checks and error
-messages (src/taomate_hd/inference/fused_kernels.py:826-873) and runs the
-gfx950 kernel behind ``tmhd_qkv_norm_rope`` in place on the current stream.
-The arithmetic and bf16 rounding follow the reference's Triton kernel
-(``:425-472``); the order of the sum of squares and a correctly rounded
+``fused_qkv_qk_norm_rope_`` (in place in the merged QKV projection) and
+``fused_qk_norm_rope`` (one projection, new output) have the reference's
+signatures, checks and error messages
+(src/taomate_hd/inference/fused_kernels.py:798-873) and run the gfx950 kernels
+behind ``tmhd_qkv_norm_rope`` / ``tmhd_qk_norm_rope`` on the current stream.
+The arithmetic and bf16 rounding follow the reference's Triton kernels
+(``:385-472``); the order of the sum of squares and a correctly rounded
 inverse square root are fixed where the reference leaves them to its
 compiler (stated in include/tmhd.h).
 """
@@ -57,3 +59,42 @@ def fused_qkv_qk_norm_rope_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cach
     )
     _native.check(status, "tmhd_qkv_norm_rope")
     return qkv
+
+
+def fused_qk_norm_rope(value: Any, weight: Any, cos: Any, sin: Any, eps: float) -> Any:
+    """RMSNorm + RoPE of one projection ``value [tokens, heads, head_dim]``
+    (bf16; rows may be strided, e.g. the Q or K view of a merged projection)
+    into a new contiguous bf16 tensor.  ``cos`` / ``sin`` are
+    ``[tokens, rotary_dim]`` per-channel tables; a float dtype other than
+    bf16 is rounded to bf16 first, which is the reference kernel's own
+    rounding of them (``_round_bf16`` on load).  ``weight`` must be bf16: the
+    reference uses a wider weight unrounded, which this kernel does not.
+    """
+    import torch
+
+    tokens, heads, head_dim = value.shape
+    rotary_dim = int(cos.shape[-1])
+    if rotary_dim > head_dim or rotary_dim % 2:
+        raise ValueError("SOL QKNorm/RoPE requires an even rotary span within a head")
+    if value.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise ValueError("fused QK norm/RoPE requires a BF16 value and weight")
+    if weight.ndim != 1 or int(weight.numel()) != head_dim:
+        raise ValueError("fused QK norm weight does not match head_dim")
+    if value.stride(-1) != 1 or value.stride(1) != head_dim:
+        value = value.contiguous()
+    if int(cos.numel()) != tokens * rotary_dim or int(sin.numel()) != tokens * rotary_dim:
+        raise ValueError("fused QK RoPE tables do not cover every token")
+    cos = cos.to(torch.bfloat16).reshape(tokens, rotary_dim).contiguous()
+    sin = sin.to(torch.bfloat16).reshape(tokens, rotary_dim).contiguous()
+    for name, t in (("value", value), ("weight", weight), ("cos", cos), ("sin", sin)):
+        if t.device != value.device or t.device.type != "cuda":
+            raise ValueError(f"{name} must be on the GPU of value")
+    weight = weight.contiguous()
+    out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=value.device)
+    status = _native.load().tmhd_qk_norm_rope(
+        _native.ptr(value), tokens, heads, head_dim, value.stride(0), _native.ptr(out), out.stride(0),
+        _native.ptr(weight), _native.ptr(cos), cos.stride(0), _native.ptr(sin), sin.stride(0), rotary_dim,
+        float(eps), _native.stream_ptr(torch, value.device),
+    )
+    _native.check(status, "tmhd_qk_norm_rope")
+    return out

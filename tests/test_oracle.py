@@ -388,3 +388,40 @@ def test_qkv_norm_rope_partial_rotary_and_weights_select_q_k():
     inv = np.float32(1) / np.sqrt(orope.sum_squares(x, R) / np.float32(D) + np.float32(1e-6))
     assert np.array_equal(sw[:, 0], orope.round_bf16((x[:, 0] * inv[:, 0, :, None]) * kw))
     assert np.array_equal(nrm[:, 1], orope.round_bf16((x[:, 1] * inv[:, 1, :, None]) * kw))
+
+
+def test_qk_norm_rope_equals_merged_form_with_duplicated_tables():
+    # the model's unmerged path builds per-token tables by repeating the cache
+    # halves (model/layers.py:415-420); both reference kernels must then agree
+    qkv, qw, kw, cache, pos = _rope_case(rotary=96)
+    T, H, D, R = 7, 3, 128, 96
+    merged = orope.qkv_norm_rope(qkv, qw, kw, cache, pos, 1e-6, H)[:, : 2 * H * D].reshape(T, 2, H, D)
+    rows = cache[pos]
+    cos = np.concatenate([rows[:, : R // 2], rows[:, : R // 2]], -1)
+    sin = np.concatenate([rows[:, R // 2:], rows[:, R // 2:]], -1)
+    x = qkv[:, : 2 * H * D].reshape(T, 2, H, D)
+    assert np.array_equal(orope.qk_norm_rope(x[:, 0], qw, cos, sin, 1e-6), merged[:, 0])
+    assert np.array_equal(orope.qk_norm_rope(x[:, 1], kw, cos, sin, 1e-6), merged[:, 1])
+
+
+def test_qk_norm_rope_per_channel_tables_closed_form():
+    rng = np.random.default_rng(8)
+    T, H, D, R = 5, 2, 64, 48
+    x = bf16.round_f32(rng.standard_normal((T, H, D)).astype(np.float32))
+    w = bf16.round_f32(1 + 0.1 * rng.standard_normal(D).astype(np.float32))
+    ang = rng.uniform(-3, 3, (T, R))  # every channel its own angle
+    cos = bf16.round_f32(np.cos(ang).astype(np.float32))
+    sin = bf16.round_f32(np.sin(ang).astype(np.float32))
+    out = orope.qk_norm_rope(x, w, cos, sin, 1e-6).astype(np.float64)
+    n = orope.qk_norm_rope(x, w, np.ones((T, R), np.float32), np.zeros((T, R), np.float32), 1e-6).astype(np.float64)
+    h = R // 2
+    c, s = cos[:, None, :].astype(np.float64), sin[:, None, :].astype(np.float64)
+    want_lo = n[..., :h] * c[..., :h] - n[..., h:R] * s[..., :h]
+    want_hi = n[..., h:R] * c[..., h:] + n[..., :h] * s[..., h:]
+    tol = 2.0 ** -6 * (np.abs(n[..., :h]) + np.abs(n[..., h:R])) + 1e-30
+    assert np.all(np.abs(out[..., :h] - want_lo) <= tol)
+    assert np.all(np.abs(out[..., h:R] - want_hi) <= tol)
+    assert np.array_equal(out[..., R:], n[..., R:])
+    # float32 tables are rounded to bf16 on load: identical to pre-rounded tables
+    cos32, sin32 = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    assert np.array_equal(orope.qk_norm_rope(x, w, cos32, sin32, 1e-6), orope.qk_norm_rope(x, w, cos, sin, 1e-6))

@@ -29,7 +29,8 @@ def _case(tokens, heads, head_dim, rotary, seed, npos=23):
 
 @pytest.mark.parametrize(
     "tokens,heads,head_dim,rotary,eps",
-    [(37, 5, 128, 128, 1e-6), (64, 3, 128, 64, 1e-5), (20, 4, 64, 64, 1e-6), (9, 2, 64, 32, 1e-6), (5, 3, 128, 0, 1e-6)],
+    [(37, 5, 128, 128, 1e-6), (64, 3, 128, 64, 1e-5), (20, 4, 64, 64, 1e-6), (9, 2, 64, 32, 1e-6), (5, 3, 128, 0, 1e-6),
+     (33, 6, 128, 96, 1e-6), (11, 7, 64, 40, 1e-6), (3, 1, 128, 8, 0.0)],
 )
 def test_qkv_norm_rope_bit_exact(torch_mod, dev, tokens, heads, head_dim, rotary, eps):
     torch = torch_mod
@@ -68,3 +69,78 @@ def test_qkv_norm_rope_positions_clamped_and_checks(torch_mod, dev):
     with pytest.raises(ValueError, match="positions do not cover"):
         fused_qkv_qk_norm_rope_(t, bf16.to_torch(qw, dev), bf16.to_torch(kw, dev), bf16.to_torch(cache, dev),
                                 torch.tensor(pos[:3], device=dev), 1e-6)
+
+
+@pytest.mark.parametrize("tokens,heads,head_dim,rotary", [(29, 5, 128, 96), (16, 3, 64, 64), (7, 4, 128, 0), (13, 2, 64, 24)])
+def test_qk_norm_rope_bit_exact_strided_views(torch_mod, dev, tokens, heads, head_dim, rotary):
+    torch = torch_mod
+    from taomate_hd_amd import fused_qk_norm_rope
+
+    qkv, qw, kw, _, _ = _case(tokens, heads, head_dim, rotary, seed=3 * tokens + rotary)
+    rng = np.random.default_rng(tokens)
+    ang = rng.uniform(-5, 5, (tokens, rotary))  # per-channel tables: both halves differ
+    cos = bf16.round_f32(np.cos(ang).astype(np.float32))
+    sin = bf16.round_f32(np.sin(ang).astype(np.float32))
+    t = bf16.to_torch(qkv, dev)
+    width = heads * head_dim
+    q = t[:, :width].view(tokens, heads, head_dim)          # strided rows of the merged buffer
+    k = t[:, width : 2 * width].view(tokens, heads, head_dim)
+    before = t.clone()
+    for view, w, part in ((q, qw, 0), (k, kw, 1)):
+        out = fused_qk_norm_rope(view, bf16.to_torch(w, dev), bf16.to_torch(cos, dev).reshape(tokens, rotary),
+                                 bf16.to_torch(sin, dev).reshape(tokens, rotary), 1e-6)
+        torch.cuda.synchronize()
+        assert out.is_contiguous() and tuple(out.shape) == (tokens, heads, head_dim)
+        x = qkv[:, part * width : (part + 1) * width].reshape(tokens, heads, head_dim)
+        want = orope.qk_norm_rope(x, w, cos, sin, 1e-6)
+        assert np.array_equal(bf16.from_torch(out).view(np.uint32), want.view(np.uint32))
+    assert torch.equal(t, before)  # the source projection is only read
+    # float32 tables: rounded to bf16 first, as the reference kernel rounds them on load
+    out32 = fused_qk_norm_rope(q, bf16.to_torch(qw, dev), torch.tensor(np.cos(ang), dtype=torch.float32, device=dev),
+                               torch.tensor(np.sin(ang), dtype=torch.float32, device=dev), 1e-6)
+    want = orope.qk_norm_rope(qkv[:, :width].reshape(tokens, heads, head_dim), qw, cos, sin, 1e-6)
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16.from_torch(out32).view(np.uint32), want.view(np.uint32))
+
+
+def test_qk_norm_rope_in_place_and_overlap_refused(torch_mod, dev):
+    torch = torch_mod
+    from taomate_hd_amd import _native
+
+    tokens, heads, head_dim, rotary = 10, 3, 128, 96
+    qkv, qw, _, _, _ = _case(tokens, heads, head_dim, rotary, seed=4)
+    rng = np.random.default_rng(5)
+    ang = rng.uniform(-5, 5, (tokens, rotary))
+    cos = bf16.round_f32(np.cos(ang).astype(np.float32))
+    sin = bf16.round_f32(np.sin(ang).astype(np.float32))
+    width = heads * head_dim
+    x = bf16.to_torch(np.ascontiguousarray(qkv[:, :width]), dev)
+    w, c, s = bf16.to_torch(qw, dev), bf16.to_torch(cos, dev), bf16.to_torch(sin, dev)
+    lib = _native.load()
+    stream = _native.stream_ptr(torch, dev)
+    st = lib.tmhd_qk_norm_rope(_native.ptr(x), tokens, heads, head_dim, width, _native.ptr(x), width, _native.ptr(w),
+                               _native.ptr(c), rotary, _native.ptr(s), rotary, rotary, 1e-6, stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    want = orope.qk_norm_rope(qkv[:, :width].reshape(tokens, heads, head_dim), qw, cos, sin, 1e-6)
+    assert np.array_equal(bf16.from_torch(x).reshape(tokens, heads, head_dim).view(np.uint32), want.view(np.uint32))
+    # out shifted by one row onto value: refused, nothing launched
+    st = lib.tmhd_qk_norm_rope(_native.ptr(x), tokens - 1, heads, head_dim, width, _native.ptr(x) + 2 * width, width,
+                               _native.ptr(w), _native.ptr(c), rotary, _native.ptr(s), rotary, rotary, 1e-6, stream)
+    assert st != 0 and b"overlaps" in lib.tmhd_last_error()
+    st = lib.tmhd_qk_norm_rope(_native.ptr(x), tokens, heads, head_dim, width, _native.ptr(x), width, _native.ptr(w),
+                               _native.ptr(c), rotary, _native.ptr(s), rotary, 12, 1e-6, stream)
+    assert st != 0 and b"rotary_dim" in lib.tmhd_last_error()
+
+
+def test_rounding_helpers_exhaustive(torch_mod, dev):
+    # all 2^32 patterns: the bf16 conversion equals the reference's integer
+    # rounding and the square root is correctly rounded
+    torch = torch_mod
+    from taomate_hd_amd import _native
+
+    counts = torch.zeros(2, dtype=torch.int64, device=dev)
+    _native.check(_native.load().tmhd_selfcheck_rounding(_native.ptr(counts), _native.stream_ptr(torch, dev)),
+                  "tmhd_selfcheck_rounding")
+    torch.cuda.synchronize()
+    assert counts.tolist() == [0, 0]
