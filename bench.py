@@ -190,6 +190,24 @@ def bench_rope(torch, dev, steps, warmup):
     return dev_ms
 
 
+def bench_packed(torch, dev, steps, warmup):
+    """Dense attention over two 768p-chunk documents of a packed sequence
+    (packed_sdpa: K/V pack + one BF16 kernel launch per document), synthetic
+    bf16 inputs; returns (ms per call, flop per call)."""
+    from taomate_hd_amd import packed_sdpa
+
+    gen = torch.Generator(device=dev).manual_seed(9)
+    docs = (LQ, LQ)
+    total = sum(docs)
+    qkv = _randn(torch, (total, 3 * H * D), gen, dev).to(torch.bfloat16)
+    q, k, v = (qkv[:, i * H * D : (i + 1) * H * D].view(total, H, D) for i in range(3))
+    bounds = (0, docs[0], total)
+    _, dev_ms = time_steps(
+        torch, lambda: packed_sdpa(q, k, v, cu_seqlens=None, cu_seqlens_host=bounds, max_seqlen=max(docs),
+                                   scale=D ** -0.5), steps, warmup)
+    return dev_ms, 4.0 * H * D * sum(n * n for n in docs)
+
+
 def cpu_baseline(torch):
     """The reference serial backend (torch SDPA, fp32) on the host cores over the 768p attention.
 
@@ -240,7 +258,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "copy"), default="all")
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "packed", "copy"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -379,6 +397,17 @@ def main() -> int:
         if result["value"] is None:
             result["value"], result["ms_per_step"] = result["qkv_norm_rope"]["gbps"], round(rope_ms, 4)
             result["unit"] = "GB/s"
+    if args.workload in ("all", "packed"):
+        packed_ms, packed_flop = bench_packed(torch, dev, args.steps, args.warmup)
+        result["packed_sdpa"] = {
+            "ms_per_call": round(packed_ms, 4),
+            "tflops": round(packed_flop / (packed_ms * 1e-3) / 1e12, 1),
+            "shape": f"2 documents x {LQ} tokens, heads {H}, head_dim {D}, K/V pack included",
+        }
+        _log(f"packed sdpa: {packed_ms:.3f} ms per call")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["packed_sdpa"]["tflops"], round(packed_ms, 4)
+            result["unit"] = "TFLOPS"
     if not args.no_cpu_baseline and args.workload in ("all", "bf16"):
         result["cpu_baseline"] = cpu_baseline(torch)
         _log(f"cpu baseline: {result['cpu_baseline']}")

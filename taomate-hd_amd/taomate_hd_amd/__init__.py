@@ -29,6 +29,7 @@ from .kvcache import (
     KVContract,
     kv_contract_from_model,
 )
+from .packed import packed_sdpa
 from .rope import fused_qk_norm_rope, fused_qkv_qk_norm_rope_
 from .quant import (
     cutlass_scaled_mm,
@@ -52,6 +53,7 @@ from .w8a8 import (
 
 __all__ = [
     "fused_qk_norm_rope",
+    "packed_sdpa",
     "fused_qkv_qk_norm_rope_",
     "_native",
     "AVKV",

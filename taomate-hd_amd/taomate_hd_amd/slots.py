@@ -35,16 +35,24 @@ def vt_position(t: int) -> int:
 
 @dataclass
 class SlotView:
-    """The first ``tokens`` rows of a slot, as one attention segment."""
+    """Rows ``row0 .. row0 + tokens`` of a slot, as one attention segment.
+
+    ``row0`` is a multiple of 64 (a key tile; the transposed value order
+    repeats every 16 tokens), and the slot rows up to the next multiple of 64
+    after the view are zero.
+    """
 
     slot: "KVSlot"
     tokens: int
+    row0: int = 0
 
     def to_segment(self) -> _native.KVSegment:
         s = self.slot
+        if self.row0 % KV_TILE or self.row0 + round_up(self.tokens, KV_TILE) > s.capacity:
+            raise ValueError(f"slot view rows [{self.row0}, {self.row0 + self.tokens}) are not a tile-aligned part of the slot")
         return _native.KVSegment(
-            k=_native.ptr(s.k),
-            vt=_native.ptr(s.vt),
+            k=_native.ptr(s.k) + 2 * self.row0 * s.head_dim,
+            vt=_native.ptr(s.vt) + 2 * self.row0,
             k_head_stride=s.capacity * s.head_dim,
             vt_head_stride=s.capacity * s.head_dim,
             vt_row_stride=s.capacity,
@@ -75,11 +83,14 @@ class KVSlot:
             raise ValueError(f"slot view of {count} tokens outside the {self.tokens} packed rows")
         return SlotView(self, count)
 
-    def pack(self, key: Any, value: Any, *, rows: Any | None = None, row0: int = 0, count: int | None = None) -> None:
+    def pack(self, key: Any, value: Any, *, rows: Any | None = None, row0: int = 0, count: int | None = None,
+             dst: int = 0) -> None:
         """Copy token-major rows of ``key``/``value`` ([T, H, D] bf16) into the slot.
 
         ``rows`` is an int32/int64 GPU index tensor; without it rows
-        ``row0 .. row0 + count`` are copied.
+        ``row0 .. row0 + count`` are copied.  They land at slot rows
+        ``dst ..`` (``dst`` a multiple of 64) and the slot rows after them up to
+        the next multiple of 64 are zeroed; ``tokens`` becomes the end row.
         """
         torch = self._torch
         for name, t in (("key", key), ("value", value)):
@@ -101,17 +112,18 @@ class KVSlot:
             n = int(key.shape[0]) - int(row0) if count is None else int(count)
             if int(row0) < 0 or n < 0 or int(row0) + n > int(key.shape[0]):
                 raise ValueError(f"rows [{row0}, {int(row0) + n}) outside the {int(key.shape[0])} K/V rows")
-        if n > self.capacity:
-            raise ValueError(f"{n} rows exceed the slot capacity {self.capacity}")
+        dst = int(dst)
+        if dst < 0 or dst % KV_TILE or dst + n > self.capacity:
+            raise ValueError(f"{n} rows at slot row {dst} do not fit the slot capacity {self.capacity} (tile-aligned)")
         lib = _native.load()
         status = lib.tmhd_kv_pack(
             _native.ptr(key), _native.ptr(value), key.stride(0), key.stride(1), rows_ptr, int(row0), n,
             _native.ptr(self.k), _native.ptr(self.vt), self.capacity * self.head_dim,
-            self.capacity * self.head_dim, self.capacity, 0, round_up(n, KV_TILE), self.heads,
+            self.capacity * self.head_dim, self.capacity, dst, dst + round_up(n, KV_TILE), self.heads,
             self.head_dim, _native.stream_ptr(torch, key.device),
         )
         _native.check(status, "tmhd_kv_pack")
-        self.tokens = n
+        self.tokens = dst + n
 
     def token_major(self, tokens: int | None = None, order: Any | None = None) -> tuple[Any, Any]:
         """Materialise ``[tokens, H, D]`` key/value copies (compatibility path)."""

@@ -232,3 +232,18 @@ def test_build_recipe_targets_gfx950_without_packed_fp32():
     spec.loader.exec_module(mod)
     assert "--offload-arch=gfx950" in mod.HIPCC_FLAGS
     assert "-packed-fp32-ops" in mod.HIPCC_FLAGS
+
+
+def test_packed_sdpa_boundary_validation_without_gpu():
+    import torch
+    from taomate_hd_amd import packed_sdpa
+
+    q = torch.zeros((10, 2, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="cumulative lengths are invalid"):
+        packed_sdpa(q, q, q, cu_seqlens=torch.tensor([0, 4, 9]), cu_seqlens_host=None, max_seqlen=5, scale=0.1)
+    with pytest.raises(ValueError, match="cumulative lengths are invalid"):
+        packed_sdpa(q, q, q, cu_seqlens=None, cu_seqlens_host=(0, 6, 4, 10), max_seqlen=6, scale=0.1)
+    with pytest.raises(ValueError, match="no live segment"):
+        packed_sdpa(q[:0], q[:0], q[:0], cu_seqlens=None, cu_seqlens_host=(0, 0, 0), max_seqlen=0, scale=0.1)
+    with pytest.raises(ValueError, match="GPU tensor"):  # valid boundaries: the HIP path is required
+        packed_sdpa(q, q, q, cu_seqlens=None, cu_seqlens_host=(0, 4, 10), max_seqlen=6, scale=0.1)
