@@ -38,6 +38,8 @@ H, D = 40, 128
 # rotary span of the DiT: cos / sin of 3 position axes x 16 frequencies, both halves
 # (model/architecture.py:31, model/layers.py:150-165)
 ROTARY = 96
+# DiT hidden width (model/architecture.py:18)
+HIDDEN = 5376
 LQ = 12252  # 3 latent frames x 48 x 84 video tokens + 156 audio tokens
 VIDEO, AUDIO = 12096, 156
 ANCHOR = 4032
@@ -208,6 +210,28 @@ def bench_packed(torch, dev, steps, warmup):
     return dev_ms, 4.0 * H * D * sum(n * n for n in docs)
 
 
+def bench_adaln(torch, dev, steps, warmup):
+    """The DiT block's row ops around one attention call on the 768p chunk's
+    hidden rows (LQ x 5376, bf16, AdaLN tables as strided chunks of one
+    projection): pre-attention RMSNorm + modulate and post-attention residual
+    gate + RMSNorm + modulate.  Returns {name: (ms per call, bytes per call)}."""
+    from taomate_hd_amd import fused_residual_gate_rms_norm_modulate, fused_rms_norm_modulate
+
+    cols = HIDDEN
+    gen = torch.Generator(device=dev).manual_seed(10)
+    x = _randn(torch, (LQ, cols), gen, dev).to(torch.bfloat16)
+    branch = _randn(torch, (LQ, cols), gen, dev).to(torch.bfloat16)
+    w = (1.0 + 0.1 * _randn(torch, (cols,), gen, dev)).to(torch.bfloat16)
+    proj = (0.3 * _randn(torch, (2, 6 * cols), gen, dev)).to(torch.bfloat16)
+    t = [proj[:, i * cols : (i + 1) * cols] for i in range(6)]
+    idx = (torch.arange(LQ, device=dev) >= LQ // 2).long()
+    row_bytes = LQ * cols * 2
+    _, pre_ms = time_steps(torch, lambda: fused_rms_norm_modulate(x, w, t[1], t[0], idx, 1e-6), steps, warmup)
+    _, post_ms = time_steps(
+        torch, lambda: fused_residual_gate_rms_norm_modulate(x, branch, t[2], w, t[4], t[3], idx, 1e-6), steps, warmup)
+    return {"rms_norm_modulate": (pre_ms, 2 * row_bytes), "residual_gate_rms_norm_modulate": (post_ms, 4 * row_bytes)}
+
+
 def cpu_baseline(torch):
     """The reference serial backend (torch SDPA, fp32) on the host cores over the 768p attention.
 
@@ -258,7 +282,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "packed", "copy"), default="all")
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "copy"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -396,6 +420,20 @@ def main() -> int:
         _log(f"qkv norm+rope: {rope_ms * 1e3:.1f} us per call")
         if result["value"] is None:
             result["value"], result["ms_per_step"] = result["qkv_norm_rope"]["gbps"], round(rope_ms, 4)
+            result["unit"] = "GB/s"
+    if args.workload in ("all", "adaln"):
+        result["adaln_rows"] = {}
+        for name, (ms, nbytes) in bench_adaln(torch, dev, args.steps, args.warmup).items():
+            result["adaln_rows"][name] = {
+                "us_per_call": round(ms * 1e3, 1),
+                "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            }
+            _log(f"{name}: {ms * 1e3:.1f} us per call")
+        result["adaln_rows"]["shape"] = f"rows {LQ}, cols {HIDDEN}, 2 table rows"
+        if result["value"] is None:
+            r = result["adaln_rows"]["residual_gate_rms_norm_modulate"]
+            result["value"], result["ms_per_step"] = r["gbps"], round(r["us_per_call"] / 1e3, 4)
             result["unit"] = "GB/s"
     if args.workload in ("all", "packed"):
         packed_ms, packed_flop = bench_packed(torch, dev, args.steps, args.warmup)

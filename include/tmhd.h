@@ -207,6 +207,55 @@ int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t 
                       void *stream);
 
 /*
+ * Row-wise bf16 ops of the DiT block around each attention call: `rows`
+ * rows of `cols` columns (row strides in elements), bf16 weight [cols],
+ * bf16 tables scale / shift / gate [table_rows][*] read at row t =
+ * index[row] (int64, clamped to [0, table_rows)).  With R() the bf16
+ * round-to-nearest-even and inv = 1 / sqrt(sum(x^2) / cols + eps):
+ *   tmhd_rms_norm:          out = R((x * inv) * w)
+ *   tmhd_rms_norm_modulate: n = R((x * inv) * w),
+ *                           out = R(R(n * R(1 + scale[t])) + shift[t])
+ *   tmhd_residual_gate_rms_norm_modulate:
+ *                           hidden = R(residual + R(gate[t] * branch)), then
+ *                           out = the rms_norm_modulate of hidden
+ *   tmhd_modulate:          out = R(R(x * R(1 + scale[t])) + shift[t])
+ *   tmhd_gate_add:          out = R(residual + R(gate[t] * branch))
+ * The sum of squares is fixed: the row's 8-column chunks are dealt to 64
+ * partials (chunk c to partial c % 64), each a chain of fused multiply-adds
+ * over its chunks in order, added as a pairwise tree in order; the square
+ * root and divisions are correctly rounded.
+ * Replace fused_rms_norm, fused_rms_norm_modulate,
+ * fused_residual_gate_rms_norm_modulate, fused_modulate and fused_gate_add
+ * with their kernels, src/taomate_hd/inference/fused_kernels.py:220-253,
+ * 312-382, 636-795.
+ * cols a multiple of 8 up to 8192; pointers and row strides 16-byte aligned.
+ */
+int tmhd_rms_norm(const void *x, int64_t x_stride, void *out, int64_t out_stride,
+                  const void *weight, int64_t rows, int32_t cols, float eps, void *stream);
+int tmhd_rms_norm_modulate(const void *x, int64_t x_stride, void *out, int64_t out_stride,
+                           const void *weight, const void *scale, int64_t scale_stride,
+                           const void *shift, int64_t shift_stride, const int64_t *index,
+                           int64_t table_rows, int64_t rows, int32_t cols, float eps,
+                           void *stream);
+int tmhd_residual_gate_rms_norm_modulate(const void *residual, int64_t residual_stride,
+                                         const void *branch, int64_t branch_stride,
+                                         const void *gate, int64_t gate_stride,
+                                         const void *weight, const void *scale,
+                                         int64_t scale_stride, const void *shift,
+                                         int64_t shift_stride, const int64_t *index,
+                                         int64_t table_rows, void *hidden,
+                                         int64_t hidden_stride, void *out, int64_t out_stride,
+                                         int64_t rows, int32_t cols, float eps, void *stream);
+int tmhd_modulate(const void *x, int64_t x_stride, void *out, int64_t out_stride,
+                  const void *scale, int64_t scale_stride, const void *shift,
+                  int64_t shift_stride, const int64_t *index, int64_t table_rows, int64_t rows,
+                  int32_t cols, void *stream);
+int tmhd_gate_add(const void *residual, int64_t residual_stride, const void *gate,
+                  int64_t gate_stride, const void *branch, int64_t branch_stride,
+                  const int64_t *index, int64_t table_rows, void *out, int64_t out_stride,
+                  int64_t rows, int32_t cols, void *stream);
+
+/*
  * No counterpart in the reference: a device self-check for deployments and
  * tests.  Runs every one of the 2^32 float bit patterns through the two
  * rounding helpers the norm + RoPE kernels depend on and adds the failures

@@ -4,7 +4,10 @@ A drop-in for the reference's per-layer streaming attention hook
 (src/taomate_hd/streaming/attention_hook.py), its clean audio-video KV cache
 (streaming/cache.py), the session around them (streaming/session.py,
 capability.py, policy.py) and the selective W8A8 projection ops
-(inference/w8a8.py, distributed/linear.py ``_linear``).  All compute runs in
+(inference/w8a8.py, distributed/linear.py ``_linear``), plus the DiT block's
+fused row ops around each attention call (Q/K norm + RoPE, RMSNorm / AdaLN /
+residual gate; inference/fused_kernels.py) and the dense packed attention of
+non-streamed forwards (model/layers.py ``_packed_sdpa``).  All compute runs in
 the hand-written HIP kernels of libtmhd.so; nothing falls back to the CPU.
 """
 
@@ -29,6 +32,13 @@ from .kvcache import (
     KVContract,
     kv_contract_from_model,
 )
+from .adaln import (
+    fused_gate_add,
+    fused_modulate,
+    fused_residual_gate_rms_norm_modulate,
+    fused_rms_norm,
+    fused_rms_norm_modulate,
+)
 from .packed import packed_sdpa
 from .rope import fused_qk_norm_rope, fused_qkv_qk_norm_rope_
 from .quant import (
@@ -52,7 +62,12 @@ from .w8a8 import (
 )
 
 __all__ = [
+    "fused_gate_add",
+    "fused_modulate",
     "fused_qk_norm_rope",
+    "fused_residual_gate_rms_norm_modulate",
+    "fused_rms_norm",
+    "fused_rms_norm_modulate",
     "packed_sdpa",
     "fused_qkv_qk_norm_rope_",
     "_native",

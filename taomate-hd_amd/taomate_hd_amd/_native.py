@@ -89,6 +89,27 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             c_int32, c_int32, c_void_p,
         ],
     ),
+    "tmhd_rms_norm": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int32, c_float, c_void_p]),
+    "tmhd_rms_norm_modulate": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+         c_int64, c_int32, c_float, c_void_p],
+    ),
+    "tmhd_residual_gate_rms_norm_modulate": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
+         c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int32, c_float, c_void_p],
+    ),
+    "tmhd_modulate": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+         c_int32, c_void_p],
+    ),
+    "tmhd_gate_add": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+         c_int32, c_void_p],
+    ),
     "tmhd_selfcheck_rounding": (c_int, [c_void_p, c_void_p]),
     "tmhd_qk_norm_rope": (
         c_int,

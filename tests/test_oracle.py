@@ -425,3 +425,81 @@ def test_qk_norm_rope_per_channel_tables_closed_form():
     # float32 tables are rounded to bf16 on load: identical to pre-rounded tables
     cos32, sin32 = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
     assert np.array_equal(orope.qk_norm_rope(x, w, cos32, sin32, 1e-6), orope.qk_norm_rope(x, w, cos, sin, 1e-6))
+
+
+# ---------------------------------------------------------------- RMSNorm / AdaLN / gate rows
+from oracle import adaln as oada  # noqa: E402
+
+
+def test_row_sum_order_hand_cases():
+    # 2^12 in chunk 0 (partial 0) and ones in chunk 1 (partial 1): partial 0
+    # stays 2^24 (each + 1 ties back to even), the tree adds 8 -> 2^24 + 8.
+    # One sequential chain over both chunks would give 2^24.
+    y = np.zeros((1, 16), np.float32)
+    y[0, 0] = 2.0 ** 12
+    y[0, 1:8] = 1.0
+    y[0, 8:] = 1.0
+    assert oada.sum_squares_row(y)[0] == np.float32(2.0 ** 24 + 8.0)
+    # two rounds: partial 0 holds chunks 0 then 64, in that order; ones first
+    # (8), then 2^24 -> 2^24 + 8, and the ones after it tie back: 2^24 + 8.
+    # Chunk 64 first would give 2^24.
+    z = np.zeros((1, 1024), np.float32)
+    z[0, :8] = 1.0
+    z[0, 512] = 2.0 ** 12
+    z[0, 513:520] = 1.0
+    assert oada.sum_squares_row(z)[0] == np.float32(2.0 ** 24 + 8.0)
+    # fused multiply-add inside a partial (see the rope case)
+    f = np.zeros((1, 16), np.float32)
+    f[0, 0], f[0, 1] = 2.0 ** -59, 2.0 ** -68 * (1 + 2.0 ** -7)
+    assert oada.sum_squares_row(f)[0] == np.float32(2.0 ** -118 + 2.0 ** -136 + 2.0 ** -141)
+    # random rows: float64 agreement
+    x = np.random.default_rng(3).standard_normal((20, 5376)).astype(np.float32)
+    want = (x.astype(np.float64) ** 2).sum(-1)
+    assert np.all(np.abs(oada.sum_squares_row(x) - want) <= 1e-5 * want)
+
+
+def test_modulate_and_gate_add_equal_the_reference_eager_bf16_path():
+    # the reference's unfused fallback (model/layers.py:126-128, 146) runs in
+    # bf16 torch, which rounds after every op: the fused kernels' R() chain
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(11)
+    rows, cols, trows = 37, 256, 3
+    x = bf16.round_f32(rng.standard_normal((rows, cols)).astype(np.float32) * 3)
+    br = bf16.round_f32(rng.standard_normal((rows, cols)).astype(np.float32))
+    scale = bf16.round_f32(rng.standard_normal((trows, cols)).astype(np.float32) * 0.3)
+    shift = bf16.round_f32(rng.standard_normal((trows, cols)).astype(np.float32) * 0.3)
+    gate = bf16.round_f32(rng.standard_normal((trows, cols)).astype(np.float32))
+    idx = rng.integers(0, trows, rows)
+    t = lambda a: torch.tensor(a, dtype=torch.float32).to(torch.bfloat16)
+    ti = torch.tensor(idx, dtype=torch.long)
+    eager_mod = (t(x) * (1.0 + t(scale).index_select(0, ti)) + t(shift).index_select(0, ti)).to(torch.bfloat16)
+    eager_gate = (t(x) + t(gate).index_select(0, ti) * t(br)).to(torch.bfloat16)
+    assert np.array_equal(oada.modulate(x, scale, shift, idx), eager_mod.float().numpy())
+    assert np.array_equal(oada.gate_add(x, gate, br, idx), eager_gate.float().numpy())
+
+
+def test_rms_norm_family_closed_forms():
+    rng = np.random.default_rng(12)
+    rows, cols = 9, 5376
+    x = bf16.round_f32(rng.standard_normal((rows, cols)).astype(np.float32) * 2)
+    w = bf16.round_f32(1 + 0.1 * rng.standard_normal(cols).astype(np.float32))
+    out = oada.rms_norm(x, w, 1e-6).astype(np.float64)
+    x64 = x.astype(np.float64)
+    ref = x64 / np.sqrt((x64 * x64).mean(-1, keepdims=True) + 1e-6) * w
+    assert np.all(np.abs(out - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-30)
+    # constant rows: x * inv = sign(x) within float rounding; eps pulls a zero row to zero
+    c = np.full((2, 64), 3.0, np.float32)
+    c[1] = 0.0
+    n = oada.rms_norm(c, np.ones(64, np.float32), 1e-6)
+    assert np.all(n[0] == 1.0) and np.all(n[1] == 0.0)
+    # modulation identities: scale 0 / shift 0 keeps the normalized row; scale -1 gives shift
+    idx = np.zeros(rows, np.int64)
+    zeros = np.zeros((1, cols), np.float32)
+    nrm = oada.rms_norm(x, w, 1e-6)
+    assert np.array_equal(oada.rms_norm_modulate(x, w, zeros, zeros, idx, 1e-6), nrm)
+    sh = bf16.round_f32(rng.standard_normal((1, cols)).astype(np.float32))
+    assert np.array_equal(oada.rms_norm_modulate(x, w, zeros - 1, sh, idx, 1e-6), np.broadcast_to(sh, x.shape))
+    # the residual form is gate-add then the same norm: gate 0 leaves the residual
+    g0 = np.zeros((1, cols), np.float32)
+    h, o = oada.residual_gate_rms_norm_modulate(x, x[::-1].copy(), g0, w, zeros, zeros, idx, 1e-6)
+    assert np.array_equal(h, x) and np.array_equal(o, nrm)
