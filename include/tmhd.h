@@ -207,6 +207,19 @@ int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t 
                       void *stream);
 
 /*
+ * The rotation alone, without the RMSNorm: out = R(R(x[d] * cos[t][d]) +
+ * R(r[d] * sin[t][d])) for d < rotary_dim (r as above, on the input values),
+ * x[d] for the other channels.  Same layout, tables and aliasing rules as
+ * tmhd_qk_norm_rope.
+ * Replaces fused_apply_rope / _rope_kernel,
+ * src/taomate_hd/inference/fused_kernels.py:257-297, 673-692.
+ */
+int tmhd_apply_rope(const void *value, int32_t tokens, int32_t heads, int32_t head_dim,
+                    int64_t value_stride, void *out, int64_t out_stride, const void *cos,
+                    int64_t cos_stride, const void *sin, int64_t sin_stride, int32_t rotary_dim,
+                    void *stream);
+
+/*
  * Row-wise bf16 ops of the DiT block around each attention call: `rows`
  * rows of `cols` columns (row strides in elements), bf16 weight [cols],
  * bf16 tables scale / shift / gate [table_rows][*] read at row t =
@@ -226,8 +239,8 @@ int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t 
  * root and divisions are correctly rounded.
  * Replace fused_rms_norm, fused_rms_norm_modulate,
  * fused_residual_gate_rms_norm_modulate, fused_modulate and fused_gate_add
- * with their kernels, src/taomate_hd/inference/fused_kernels.py:220-253,
- * 312-382, 636-795.
+ * with their kernels, src/taomate_hd/inference/fused_kernels.py:221-255,
+ * 312-383, 636-671, 706-796.
  * cols a multiple of 8 up to 8192; pointers and row strides 16-byte aligned.
  */
 int tmhd_rms_norm(const void *x, int64_t x_stride, void *out, int64_t out_stride,
@@ -254,6 +267,19 @@ int tmhd_gate_add(const void *residual, int64_t residual_stride, const void *gat
                   int64_t gate_stride, const void *branch, int64_t branch_stride,
                   const int64_t *index, int64_t table_rows, void *out, int64_t out_stride,
                   int64_t rows, int32_t cols, void *stream);
+
+/*
+ * SwiGLU of x[rows][2 * half] (gate columns, then up columns; row stride
+ * x_stride elements) into out[rows][half]: out = R(R(g * sigmoid(g)) * u),
+ * sigmoid(g) = 1 / (1 + exp(-g)) in single precision (accurate exp,
+ * correctly rounded division).  The reference's tl.sigmoid is its
+ * compiler's, so agreement is within one bf16 ulp rather than bit-exact.
+ * Replaces fused_swiglu / _swiglu_kernel,
+ * src/taomate_hd/inference/fused_kernels.py:299-310, 694-704.
+ * half a multiple of 8; pointers and row strides 16-byte aligned.
+ */
+int tmhd_swiglu(const void *x, int64_t x_stride, void *out, int64_t out_stride, int64_t rows,
+                int32_t half, void *stream);
 
 /*
  * No counterpart in the reference: a device self-check for deployments and

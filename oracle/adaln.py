@@ -4,11 +4,12 @@ Test infrastructure only: tests and the bench's CPU baseline use it as the
 checker; the product path never imports it.
 
 Restates the SOL fused kernels of src/taomate_hd/inference/fused_kernels.py:
-_modulate_kernel / fused_modulate (:220-236, 643-655), _gate_add_kernel /
-fused_gate_add (:238-253, 658-670), _rms_norm_kernel / fused_rms_norm
-(:312-321, 681-696), _rms_norm_modulate_kernel / fused_rms_norm_modulate
-(:323-347, 699-731) and _residual_gate_rms_norm_modulate_kernel /
-fused_residual_gate_rms_norm_modulate (:349-382, 734-795), with R() the
+_modulate_kernel / fused_modulate (:221-237, 643-656), _gate_add_kernel /
+fused_gate_add (:239-255, 658-671), _rms_norm_kernel / fused_rms_norm
+(:312-321, 706-721), _rms_norm_modulate_kernel / fused_rms_norm_modulate
+(:323-348, 723-755) and _residual_gate_rms_norm_modulate_kernel /
+fused_residual_gate_rms_norm_modulate (:350-383, 757-796), and
+_swiglu_kernel / fused_swiglu (:299-310, 694-704), with R() the
 reference's _round_bf16 (:58-61).  Inputs are bf16 values held as float32.
 
 Fixed here where the reference leaves it to its compiler (and matched by the
@@ -88,3 +89,15 @@ def residual_gate_rms_norm_modulate(residual: np.ndarray, branch: np.ndarray, ga
                                     eps: float) -> tuple[np.ndarray, np.ndarray]:
     hidden = gate_add(residual, gate, branch, index)
     return hidden, rms_norm_modulate(hidden, weight, scale, shift, index, eps)
+
+
+def swiglu(x: np.ndarray) -> np.ndarray:
+    """R(R(g * s) * u) over the halves (gate | up) of the last axis, with
+    s = sigmoid(g) evaluated in float64 and rounded to float32 (the reference's
+    tl.sigmoid is its compiler's approximation: parity within one bf16 ulp).
+    fused_kernels.py:299-310, 694-704."""
+    x = np.asarray(x, dtype=np.float32)
+    half = x.shape[-1] // 2
+    g, u = x[..., :half], x[..., half:]
+    s = (1.0 / (1.0 + np.exp(-g.astype(np.float64)))).astype(np.float32)
+    return round_bf16(round_bf16(g * s) * u)

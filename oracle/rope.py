@@ -4,8 +4,9 @@ Test infrastructure only: tests and the bench's CPU baseline use it as the
 checker; the product path never imports it.
 
 Restates fused_qkv_qk_norm_rope_ / _merged_qkv_preprocess_kernel
-(qkv_norm_rope) and fused_qk_norm_rope / _qk_norm_rope_kernel
-(qk_norm_rope), src/taomate_hd/inference/fused_kernels.py:385-472 and
+(qkv_norm_rope), fused_qk_norm_rope / _qk_norm_rope_kernel (qk_norm_rope)
+and fused_apply_rope / _rope_kernel (apply_rope, no norm),
+src/taomate_hd/inference/fused_kernels.py:257-297, 385-472, 673-692 and
 798-873, with the rounding helper _round_bf16 (:58-61).  For every token and
 head, Q and K (not V) of the [tokens, 3 * heads * head_dim] bf16 buffer (or
 one [tokens, heads, head_dim] projection) become
@@ -134,3 +135,22 @@ def qk_norm_rope(value: np.ndarray, weight: np.ndarray, cos: np.ndarray, sin: np
     cos_d = np.asarray(cos, np.float32)[:, None, :] if rotary else None
     sin_d = np.asarray(sin, np.float32)[:, None, :] if rotary else None
     return _norm_rope(value, np.asarray(weight, np.float32), cos_d, sin_d, rotary, eps)
+
+
+def apply_rope(value: np.ndarray, cos: np.ndarray, sin: np.ndarray) -> np.ndarray:
+    """The rotation alone on [tokens, heads, head_dim] (bf16 values as float32)
+    with per-token tables cos / sin [tokens, rotary]: channel d < rotary
+    becomes R(R(x[d] cos[d]) + R(r[d] sin[d])), r = rotate_half(x); the rest
+    is kept.  fused_kernels.py:257-297, 673-692."""
+    x = np.asarray(value, dtype=np.float32)
+    rotary = int(np.asarray(cos).shape[-1])
+    if not rotary:
+        return x.copy()
+    half = rotary // 2
+    d = np.arange(rotary)
+    paired = x[..., np.where(d < half, d + half, d - half)]
+    rotated = np.where(d < half, -paired, paired)
+    c = round_bf16(np.asarray(cos, np.float32))[:, None, :]
+    s = round_bf16(np.asarray(sin, np.float32))[:, None, :]
+    rope = round_bf16(round_bf16(x[..., :rotary] * c) + round_bf16(rotated * s))
+    return np.concatenate([rope, x[..., rotary:]], -1)

@@ -1,9 +1,9 @@
 // Row-wise bf16 RMSNorm / AdaLN-modulate / residual-gate ops of the DiT block
 // around every attention call, for gfx950.  Reference: the "SOL" fused
-// kernels of src/taomate_hd/inference/fused_kernels.py:220-253 (_modulate,
-// _gate_add), 312-382 (_rms_norm, _rms_norm_modulate,
-// _residual_gate_rms_norm_modulate) and their wrappers :636-795, with the
-// rounding helper _round_bf16 (:58-61) written R() below.
+// kernels of src/taomate_hd/inference/fused_kernels.py:221-255 (_modulate,
+// _gate_add), 312-383 (_rms_norm, _rms_norm_modulate,
+// _residual_gate_rms_norm_modulate) and their wrappers :636-671, 706-796,
+// with the rounding helper _round_bf16 (:58-61) written R() below.
 //
 //   RMS       out = R((x * inv) * w)
 //   RMS_MOD   n = R((x * inv) * w);  out = R(R(n * R(1 + scale[t])) + shift[t])
@@ -27,6 +27,8 @@
 // R() is gfx950's f32 -> bf16 conversion, which equals the reference's
 // integer rounding on every value that reaches it here (the rounding
 // self-check covers it).
+#include <algorithm>
+
 #include "tmhd_internal.h"
 
 namespace tmhd {
@@ -168,6 +170,30 @@ __global__ void __launch_bounds__(256) row_kernel(const RowArgs a) {
   }
 }
 
+// SwiGLU over [rows][2 * half] (gate | up): out = R(R(g * sigmoid(g)) * u),
+// sigmoid(g) = 1 / (1 + exp(-g)) with the accurate single-precision exp and a
+// correctly rounded division.  8 columns per thread, grid-stride.
+__global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t *x, int64_t x_stride, uint16_t *out,
+                                                     int64_t out_stride, int64_t rows, int32_t half) {
+#pragma clang fp contract(off)
+  const int64_t per_row = half >> 3;
+  const int64_t total = rows * per_row;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / per_row, c = (i - r * per_row) * 8;
+    const i32x4 g = *(const i32x4 *)(x + r * x_stride + c);
+    const i32x4 u = *(const i32x4 *)(x + r * x_stride + half + c);
+    i32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g0 = lo_f32((uint32_t)g[e]), g1 = hi_f32((uint32_t)g[e]);
+      const float s0 = __fdiv_rn(1.0f, 1.0f + expf(-g0)), s1 = __fdiv_rn(1.0f, 1.0f + expf(-g1));
+      const uint32_t act = pack_bf16_rne(g0 * s0, g1 * s1);
+      o[e] = (int)pack_bf16_rne(lo_f32(act) * lo_f32((uint32_t)u[e]), hi_f32(act) * hi_f32((uint32_t)u[e]));
+    }
+    *(i32x4 *)(out + r * out_stride + c) = o;
+  }
+}
+
 bool al16(const void *p) { return ((uintptr_t)p % 16) == 0; }
 
 template <int OP>
@@ -279,4 +305,20 @@ extern "C" int tmhd_gate_add(const void *residual, int64_t residual_stride, cons
   chk.scale = chk.shift = chk.gate, chk.scale_stride = chk.shift_stride = gate_stride;
   const int rc = check_rows("tmhd_gate_add", chk, false, true, true, false);
   return rc >= 0 ? rc : launch_rows<kGate>(a, stream, "tmhd_gate_add");
+}
+
+extern "C" int tmhd_swiglu(const void *x, int64_t x_stride, void *out, int64_t out_stride, int64_t rows, int32_t half,
+                           void *stream) {
+  const char *what = "tmhd_swiglu";
+  if (rows < 0 || half <= 0 || half % 8)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: rows %lld half %d (a multiple of 8)", what, (long long)rows, half);
+  if (rows == 0) return TMHD_OK;
+  if (!x || !out || !al16(x) || !al16(out) || x_stride % 8 || out_stride % 8 || x_stride < 2 * (int64_t)half ||
+      out_stride < half)
+    return set_error(TMHD_ERR_INVALID, "%s: pointers and row strides must be 16-byte aligned rows", what);
+  const int64_t total = rows * (half / 8);
+  const int64_t blocks = std::min<int64_t>((total + 255) / 256, 256 * 64);
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t *)x, x_stride, (uint16_t *)out, out_stride, rows, half);
+  return check_launch(what);
 }

@@ -59,7 +59,8 @@ constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad i
 
 // TABLE: cos / sin of channel d at cos_sin[positions[t]][d % h] and [h + d % h]
 // (the merged-projection form); otherwise at cos[t][d] and sin[t][d].
-template <int D, bool TABLE>
+// NORM false: the rotation alone, applied to the input values (no RMSNorm).
+template <int D, bool TABLE, bool NORM = true>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPR = D / 8;     // lanes per row
@@ -98,8 +99,11 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
     xa[u] = *(const i32x2 *)(a.src + src_off[u] + oa);
     xb[u] = *(const i32x2 *)(a.src + src_off[u] + ob);
   }
-  const i32x2 qwa = *(const i32x2 *)(a.qw + oa), qwb = *(const i32x2 *)(a.qw + ob);
-  const i32x2 kwa = *(const i32x2 *)(a.kw + oa), kwb = *(const i32x2 *)(a.kw + ob);
+  i32x2 qwa{}, qwb{}, kwa{}, kwb{};
+  if constexpr (NORM) {
+    qwa = *(const i32x2 *)(a.qw + oa), qwb = *(const i32x2 *)(a.qw + ob);
+    kwa = *(const i32x2 *)(a.kw + oa), kwb = *(const i32x2 *)(a.kw + ob);
+  }
   if (a.rotary) {
     const int ph = rotates ? 4 * j : 0;  // lanes of the unrotated tail read a valid phase, unused
 #pragma unroll
@@ -122,7 +126,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 
   float x[U][8], ss[U];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
+  for (int u = 0; u < U && NORM; ++u) {
     const uint32_t w[4] = {(uint32_t)xa[u][0], (uint32_t)xa[u][1], (uint32_t)xb[u][0], (uint32_t)xb[u][1]};
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -139,21 +143,26 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
     ss[u] = s;
   }
   // lane q of each quad computes group q's inverse RMS, then each group reads it back
-  const int q = lane & 3;
-  const float sq = q == 0 ? ss[0] : q == 1 ? ss[1] : q == 2 ? ss[2] : ss[3];
-  const float var = sq * (1.0f / D);  // exact: D is a power of two
-  const float inv_q = __fdiv_rn(1.0f, sqrt_rn(var + a.eps));
-  const float inv[U] = {dpp<0x00>(inv_q), dpp<0x55>(inv_q), dpp<0xaa>(inv_q), dpp<0xff>(inv_q)};
+  float inv[U] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if constexpr (NORM) {
+    const int q = lane & 3;
+    const float sq = q == 0 ? ss[0] : q == 1 ? ss[1] : q == 2 ? ss[2] : ss[3];
+    const float var = sq * (1.0f / D);  // exact: D is a power of two
+    const float inv_q = __fdiv_rn(1.0f, sqrt_rn(var + a.eps));
+    inv[0] = dpp<0x00>(inv_q), inv[1] = dpp<0x55>(inv_q), inv[2] = dpp<0xaa>(inv_q), inv[3] = dpp<0xff>(inv_q);
+  }
 
   const uint32_t qw[4] = {(uint32_t)qwa[0], (uint32_t)qwa[1], (uint32_t)qwb[0], (uint32_t)qwb[1]};
   const uint32_t kw[4] = {(uint32_t)kwa[0], (uint32_t)kwa[1], (uint32_t)kwb[0], (uint32_t)kwb[1]};
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    uint32_t nb[4];  // normalized, packed bf16: A pieces in 0-1, B in 2-3
+    uint32_t nb[4] = {(uint32_t)xa[u][0], (uint32_t)xa[u][1], (uint32_t)xb[u][0], (uint32_t)xb[u][1]};
+    if constexpr (NORM) {  // normalized, packed bf16: A pieces in 0-1, B in 2-3
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t w = is_k[u] ? kw[e] : qw[e];
-      nb[e] = pack_bf16((x[u][2 * e] * inv[u]) * lo_f32(w), (x[u][2 * e + 1] * inv[u]) * hi_f32(w));
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = is_k[u] ? kw[e] : qw[e];
+        nb[e] = pack_bf16((x[u][2 * e] * inv[u]) * lo_f32(w), (x[u][2 * e + 1] * inv[u]) * hi_f32(w));
+      }
     }
     uint32_t out[4] = {nb[0], nb[1], nb[2], nb[3]};
     if (a.rotary) {
@@ -187,13 +196,18 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
   }
 }
 
-int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what) {
+int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what, bool norm = true) {
   const int64_t rows = (int64_t)a.tokens * a.parts * a.heads;
   const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
   if (rows > 0x7fffffff - rows_per_block) return set_error(TMHD_ERR_UNSUPPORTED, "%s: too many rows", what);
   const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
   hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 128 && table)
+  if (!norm) {
+    if (head_dim == 128)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, false, false>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, false, false>), grid, block, 0, s, a);
+  } else if (head_dim == 128 && table)
     hipLaunchKernelGGL((qk_norm_rope_kernel<128, true>), grid, block, 0, s, a);
   else if (head_dim == 128)
     hipLaunchKernelGGL((qk_norm_rope_kernel<128, false>), grid, block, 0, s, a);
@@ -270,4 +284,38 @@ extern "C" int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t head
              (const uint16_t *)weight, (const uint16_t *)cos, (const uint16_t *)sin, cos_stride, sin_stride,
              nullptr, 0, tokens, heads, 1, rotary_dim, eps};
   return launch_rope(a, head_dim, false, stream, what);
+}
+
+extern "C" int tmhd_apply_rope(const void *value, int32_t tokens, int32_t heads, int32_t head_dim,
+                               int64_t value_stride, void *out, int64_t out_stride, const void *cos,
+                               int64_t cos_stride, const void *sin, int64_t sin_stride, int32_t rotary_dim,
+                               void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_apply_rope";
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
+  if (tokens < 0 || heads <= 0 || value_stride < (int64_t)heads * head_dim || out_stride < (int64_t)heads * head_dim)
+    return set_error(TMHD_ERR_INVALID, "%s: tokens %d heads %d strides %lld / %lld", what, tokens, heads,
+                     (long long)value_stride, (long long)out_stride);
+  if (rotary_dim < 0 || rotary_dim > head_dim || rotary_dim % 8)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: rotary_dim %d (a multiple of 8 up to head_dim)", what, rotary_dim);
+  if (tokens == 0) return TMHD_OK;
+  if (!value || !out || !aligned8(value) || !aligned8(out) || value_stride % 4 || out_stride % 4)
+    return set_error(TMHD_ERR_INVALID, "%s: value / out rows must be 8-byte aligned", what);
+  if (rotary_dim && (!cos || !sin || !aligned8(cos) || !aligned8(sin) || cos_stride % 4 || sin_stride % 4 ||
+                     cos_stride < rotary_dim || sin_stride < rotary_dim))
+    return set_error(TMHD_ERR_INVALID, "%s: cos / sin must be 8-byte aligned rows of >= rotary_dim", what);
+  if (out != value) {
+    const char *v0 = (const char *)value, *o0 = (const char *)out;
+    const int64_t vb = ((int64_t)(tokens - 1) * value_stride + (int64_t)heads * head_dim) * 2;
+    const int64_t ob = ((int64_t)(tokens - 1) * out_stride + (int64_t)heads * head_dim) * 2;
+    if (o0 < v0 + vb && v0 < o0 + ob)
+      return set_error(TMHD_ERR_INVALID, "%s: out overlaps value (only exact in-place is allowed)", what);
+  } else if (out_stride != value_stride) {
+    return set_error(TMHD_ERR_INVALID, "%s: in place needs equal strides", what);
+  }
+  RopeArgs a{(const uint16_t *)value, (uint16_t *)out, value_stride, out_stride, nullptr, nullptr,
+             (const uint16_t *)cos, (const uint16_t *)sin, cos_stride, sin_stride, nullptr, 0, tokens, heads, 1,
+             rotary_dim, 0.0f};
+  return launch_rope(a, head_dim, false, stream, what, false);
 }

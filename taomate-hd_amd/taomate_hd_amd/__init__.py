@@ -38,9 +38,10 @@ from .adaln import (
     fused_residual_gate_rms_norm_modulate,
     fused_rms_norm,
     fused_rms_norm_modulate,
+    fused_swiglu,
 )
 from .packed import packed_sdpa
-from .rope import fused_qk_norm_rope, fused_qkv_qk_norm_rope_
+from .rope import fused_apply_rope, fused_qk_norm_rope, fused_qkv_qk_norm_rope_
 from .quant import (
     cutlass_scaled_mm,
     cutlass_scaled_mm_out,
@@ -62,12 +63,14 @@ from .w8a8 import (
 )
 
 __all__ = [
+    "fused_apply_rope",
     "fused_gate_add",
     "fused_modulate",
     "fused_qk_norm_rope",
     "fused_residual_gate_rms_norm_modulate",
     "fused_rms_norm",
     "fused_rms_norm_modulate",
+    "fused_swiglu",
     "packed_sdpa",
     "fused_qkv_qk_norm_rope_",
     "_native",

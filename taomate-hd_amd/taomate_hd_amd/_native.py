@@ -110,7 +110,13 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64,
          c_int32, c_void_p],
     ),
+    "tmhd_swiglu": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int32, c_void_p]),
     "tmhd_selfcheck_rounding": (c_int, [c_void_p, c_void_p]),
+    "tmhd_apply_rope": (
+        c_int,
+        [c_void_p, c_int32, c_int32, c_int32, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64,
+         c_int32, c_void_p],
+    ),
     "tmhd_qk_norm_rope": (
         c_int,
         [

@@ -1,7 +1,7 @@
-"""Row-wise RMSNorm / AdaLN-modulate / residual-gate ops of the DiT block.
+"""Row-wise RMSNorm / AdaLN-modulate / residual-gate / SwiGLU ops of the DiT block.
 
 Drop-ins for the reference's SOL fused kernels around every attention call
-(src/taomate_hd/inference/fused_kernels.py:643-795): same signatures, checks
+(src/taomate_hd/inference/fused_kernels.py:643-671, 706-796): same signatures, checks
 and error messages, bf16 in and out, run by the gfx950 row kernels behind
 ``tmhd_rms_norm`` / ``tmhd_rms_norm_modulate`` /
 ``tmhd_residual_gate_rms_norm_modulate`` / ``tmhd_modulate`` /
@@ -60,7 +60,7 @@ def _run(status: int, what: str) -> None:
 
 
 def fused_rms_norm(value: Any, weight: Any, eps: float) -> Any:
-    """``bf16(value * rsqrt(mean(value^2) + eps) * weight)`` per row (fused_kernels.py:681-696)."""
+    """``bf16(value * rsqrt(mean(value^2) + eps) * weight)`` per row (fused_kernels.py:312-321, 706-721)."""
     import torch
 
     shape = value.shape
@@ -75,7 +75,7 @@ def fused_rms_norm(value: Any, weight: Any, eps: float) -> Any:
 
 
 def fused_rms_norm_modulate(value: Any, weight: Any, scale: Any, shift: Any, indices: Any, eps: float) -> Any:
-    """RMSNorm then AdaLN modulation with table row ``indices[row]`` (fused_kernels.py:699-731)."""
+    """RMSNorm then AdaLN modulation with table row ``indices[row]`` (fused_kernels.py:323-348, 723-755)."""
     import torch
 
     shape = value.shape
@@ -95,7 +95,7 @@ def fused_rms_norm_modulate(value: Any, weight: Any, scale: Any, shift: Any, ind
 def fused_residual_gate_rms_norm_modulate(residual: Any, branch: Any, gate: Any, weight: Any, scale: Any, shift: Any,
                                           indices: Any, eps: float) -> tuple[Any, Any]:
     """``hidden = residual + gate * branch`` (bf16 rounded), then RMSNorm + AdaLN
-    modulation of ``hidden``; returns ``(hidden, output)`` (fused_kernels.py:734-795)."""
+    modulation of ``hidden``; returns ``(hidden, output)`` (fused_kernels.py:350-383, 757-796)."""
     import torch
 
     shape = residual.shape
@@ -118,7 +118,7 @@ def fused_residual_gate_rms_norm_modulate(residual: Any, branch: Any, gate: Any,
 
 
 def fused_modulate(value: Any, shift: Any, scale: Any, indices: Any) -> Any:
-    """AdaLN modulation ``bf16(bf16(value * bf16(1 + scale[t])) + shift[t])`` (fused_kernels.py:643-655)."""
+    """AdaLN modulation ``bf16(bf16(value * bf16(1 + scale[t])) + shift[t])`` (fused_kernels.py:221-237, 643-656)."""
     import torch
 
     shape = value.shape
@@ -135,7 +135,7 @@ def fused_modulate(value: Any, shift: Any, scale: Any, indices: Any) -> Any:
 
 
 def fused_gate_add(residual: Any, gate: Any, branch: Any, indices: Any) -> Any:
-    """``bf16(residual + bf16(gate[t] * branch))`` (fused_kernels.py:658-670)."""
+    """``bf16(residual + bf16(gate[t] * branch))`` (fused_kernels.py:239-255, 658-671)."""
     import torch
 
     shape = residual.shape
@@ -152,3 +152,19 @@ def fused_gate_add(residual: Any, gate: Any, branch: Any, indices: Any) -> Any:
         _native.ptr(index), int(gate.shape[0]), _native.ptr(out), out.stride(0), rows, cols,
         _native.stream_ptr(torch, res.device)), "tmhd_gate_add")
     return out.reshape(shape)
+
+
+def fused_swiglu(value: Any) -> Any:
+    """``bf16(bf16(gate * sigmoid(gate)) * up)`` over the two halves of the last
+    axis (fused_kernels.py:299-310, 694-704); within one bf16 ulp of the
+    reference (its sigmoid is its compiler's)."""
+    import torch
+
+    shape = value.shape
+    half = int(shape[-1]) // 2
+    flat = _rows(torch, value, "value")
+    rows = int(flat.shape[0])
+    out = torch.empty((rows, half), dtype=torch.bfloat16, device=flat.device)
+    _run(_native.load().tmhd_swiglu(_native.ptr(flat), flat.stride(0), _native.ptr(out), out.stride(0), rows, half,
+                                    _native.stream_ptr(torch, flat.device)), "tmhd_swiglu")
+    return out.reshape(*shape[:-1], half)

@@ -1,10 +1,11 @@
 """Q/K RMSNorm + RoPE in front of the hook.
 
-``fused_qkv_qk_norm_rope_`` (in place in the merged QKV projection) and
-``fused_qk_norm_rope`` (one projection, new output) have the reference's
-signatures, checks and error messages
-(src/taomate_hd/inference/fused_kernels.py:798-873) and run the gfx950 kernels
-behind ``tmhd_qkv_norm_rope`` / ``tmhd_qk_norm_rope`` on the current stream.
+``fused_qkv_qk_norm_rope_`` (in place in the merged QKV projection),
+``fused_qk_norm_rope`` (one projection, new output) and ``fused_apply_rope``
+(the rotation alone) have the reference's signatures, checks and error
+messages (src/taomate_hd/inference/fused_kernels.py:673-692, 798-873) and
+run the gfx950 kernels behind ``tmhd_qkv_norm_rope`` / ``tmhd_qk_norm_rope``
+/ ``tmhd_apply_rope`` on the current stream.
 The arithmetic and bf16 rounding follow the reference's Triton kernels
 (``:385-472``); the order of the sum of squares and a correctly rounded
 inverse square root are fixed where the reference leaves them to its
@@ -97,4 +98,36 @@ def fused_qk_norm_rope(value: Any, weight: Any, cos: Any, sin: Any, eps: float) 
         float(eps), _native.stream_ptr(torch, value.device),
     )
     _native.check(status, "tmhd_qk_norm_rope")
+    return out
+
+
+def fused_apply_rope(value: Any, cos: Any, sin: Any) -> Any:
+    """The rotation alone (no RMSNorm) of ``value [tokens, heads, head_dim]``
+    bf16 with per-token tables ``cos`` / ``sin`` ``[tokens, rotary_dim]``, into a
+    new contiguous bf16 tensor (fused_kernels.py:257-297, 673-692).  Wider
+    tables are rounded to bf16 first, as the reference kernel does on load."""
+    import torch
+
+    tokens, heads, head_dim = value.shape
+    rotary_dim = int(cos.shape[-1])
+    if value.dtype != torch.bfloat16:
+        raise ValueError("fused RoPE requires a BF16 value")
+    if rotary_dim > head_dim or rotary_dim % 2:
+        raise ValueError("fused RoPE requires an even rotary span within a head")
+    if value.stride(-1) != 1 or value.stride(1) != head_dim:
+        value = value.contiguous()
+    if int(cos.numel()) != tokens * rotary_dim or int(sin.numel()) != tokens * rotary_dim:
+        raise ValueError("fused RoPE tables do not cover every token")
+    cos = cos.to(torch.bfloat16).reshape(tokens, rotary_dim).contiguous()
+    sin = sin.to(torch.bfloat16).reshape(tokens, rotary_dim).contiguous()
+    for name, t in (("value", value), ("cos", cos), ("sin", sin)):
+        if t.device != value.device or t.device.type != "cuda":
+            raise ValueError(f"{name} must be on the GPU of value")
+    out = torch.empty((tokens, heads, head_dim), dtype=torch.bfloat16, device=value.device)
+    status = _native.load().tmhd_apply_rope(
+        _native.ptr(value), tokens, heads, head_dim, value.stride(0), _native.ptr(out), out.stride(0),
+        _native.ptr(cos), cos.stride(0), _native.ptr(sin), sin.stride(0), rotary_dim,
+        _native.stream_ptr(torch, value.device),
+    )
+    _native.check(status, "tmhd_apply_rope")
     return out

@@ -80,3 +80,23 @@ def test_row_ops_index_clamp_and_checks(torch_mod, dev):
     with pytest.raises(ValueError, match="multiple of 8"):
         fused_modulate(td(x[:, :12]), td(shift[:, :12]), td(scale[:, :12]), torch.tensor(idx, device=dev))
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rows,half", [(33, 14336), (7, 64), (130, 1032)])
+def test_swiglu_within_one_bf16_ulp(torch_mod, dev, rows, half):
+    # tolerance: the reference's sigmoid is its compiler's, so the gate is one
+    # bf16 ulp everywhere and bit-identity on at least 99.9% of the elements
+    torch = torch_mod
+    from taomate_hd_amd import fused_swiglu
+
+    rng = np.random.default_rng(rows + half)
+    x = _bf(rng, (rows, 2 * half), 3.0)
+    out = fused_swiglu(bf16.to_torch(x, dev).reshape(1, rows, 2 * half))
+    torch.cuda.synchronize()
+    assert tuple(out.shape) == (1, rows, half)
+    got = bf16.from_torch(out).reshape(rows, half)
+    want = oada.swiglu(x)
+    gi, wi = got.view(np.int32).astype(np.int64), want.view(np.int32).astype(np.int64)
+    ulps = np.abs((gi >> 16) - (wi >> 16))
+    assert ulps.max() <= 1
+    assert np.mean(ulps == 0) >= 0.999

@@ -503,3 +503,36 @@ def test_rms_norm_family_closed_forms():
     g0 = np.zeros((1, cols), np.float32)
     h, o = oada.residual_gate_rms_norm_modulate(x, x[::-1].copy(), g0, w, zeros, zeros, idx, 1e-6)
     assert np.array_equal(h, x) and np.array_equal(o, nrm)
+
+
+def test_apply_rope_equals_the_reference_eager_bf16_path_and_identity():
+    # the reference's unfused rotation (model/layers.py:194-197) in bf16 torch
+    # rounds after every op: the fused kernel's R() chain
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(21)
+    T, H, D, R = 9, 3, 128, 96
+    x = bf16.round_f32(rng.standard_normal((T, H, D)).astype(np.float32) * 2)
+    ang = rng.uniform(-4, 4, (T, R // 2))
+    cos = bf16.round_f32(np.concatenate([np.cos(ang), np.cos(ang)], -1).astype(np.float32))
+    sin = bf16.round_f32(np.concatenate([np.sin(ang), np.sin(ang)], -1).astype(np.float32))
+    tb = lambda a: torch.tensor(a, dtype=torch.float32).to(torch.bfloat16)
+    rot = tb(x)[..., :R]
+    first, second = torch.chunk(rot, 2, dim=-1)
+    eager = torch.cat((rot * tb(cos)[:, None] + torch.cat((-second, first), -1) * tb(sin)[:, None], tb(x)[..., R:]), -1)
+    assert np.array_equal(orope.apply_rope(x, cos, sin), eager.float().numpy())
+    ones, zeros = np.ones((T, R), np.float32), np.zeros((T, R), np.float32)
+    assert np.array_equal(orope.apply_rope(x, ones, zeros), x)
+    # norm + rope with an identity norm weight path: qk_norm_rope = apply_rope(normalized)
+    n = orope.qk_norm_rope(x, np.ones(D, np.float32), ones, zeros, 1e-6)
+    assert np.array_equal(orope.qk_norm_rope(x, np.ones(D, np.float32), cos, sin, 1e-6), orope.apply_rope(n, cos, sin))
+
+
+def test_swiglu_closed_forms():
+    # sigmoid(0) = 1/2 -> activation 0; large positive gates pass through
+    # (g * 1), large negative gates vanish; R(R(g s) u) structure
+    g = np.array([[0.0, 20.0, -20.0, 1.0]], np.float32)
+    u = np.array([[3.0, 2.0, 5.0, 1.0]], np.float32)
+    out = oada.swiglu(np.concatenate([g, u], -1))
+    assert out[0, 0] == 0.0 and out[0, 1] == 40.0 and abs(out[0, 2]) < 1e-6
+    want = 1.0 / (1.0 + np.exp(-1.0))  # silu(1) = sigmoid(1)
+    assert abs(out[0, 3] - want) <= 2.0 ** -8 * want

@@ -144,3 +144,22 @@ def test_rounding_helpers_exhaustive(torch_mod, dev):
                   "tmhd_selfcheck_rounding")
     torch.cuda.synchronize()
     assert counts.tolist() == [0, 0]
+
+
+@pytest.mark.parametrize("tokens,heads,head_dim,rotary", [(21, 5, 128, 96), (8, 2, 64, 64), (4, 3, 128, 0)])
+def test_apply_rope_bit_exact(torch_mod, dev, tokens, heads, head_dim, rotary):
+    torch = torch_mod
+    from taomate_hd_amd import fused_apply_rope
+
+    qkv, _, _, _, _ = _case(tokens, heads, head_dim, rotary, seed=tokens * 7 + rotary)
+    rng = np.random.default_rng(tokens + 1)
+    ang = rng.uniform(-5, 5, (tokens, rotary))
+    cos = bf16.round_f32(np.cos(ang).astype(np.float32))
+    sin = bf16.round_f32(np.sin(ang).astype(np.float32))
+    width = heads * head_dim
+    t = bf16.to_torch(qkv, dev)
+    q = t[:, :width].view(tokens, heads, head_dim)
+    out = fused_apply_rope(q, bf16.to_torch(cos, dev).reshape(tokens, rotary), bf16.to_torch(sin, dev).reshape(tokens, rotary))
+    torch.cuda.synchronize()
+    want = orope.apply_rope(qkv[:, :width].reshape(tokens, heads, head_dim), cos, sin)
+    assert np.array_equal(bf16.from_torch(out).view(np.uint32), want.view(np.uint32))
