@@ -9,9 +9,14 @@ the hook packs into a slot first.  H = 40, D = 128, no mask; Q/K/V ~ N(0, 1)
 bf16 with a per-(head, channel) key offset ~ N(0, 0.5), synthetic data.
 The same step with the INT8-QK backend and the W8A8 projection
 (12,252 x 5,120 -> 13,824, per-token INT8 X, per-channel INT8 W, bf16 bias)
-are measured beside it and reported in the same JSON line.
+are measured beside it and reported in the same JSON line, together with the
+reference's own serial backend (dense K/V + torch SDPA) on the same GPU and
+inputs, the DiT block's row ops around the call (Q/K norm + RoPE, RMSNorm /
+AdaLN / residual gate) and dense packed attention.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload all|bf16|i8qk|w8a8|rope] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload all|bf16|i8qk|w8a8|rope|adaln|packed|copy]
+                    [--no-cpu-baseline] [--no-reference-gpu]
 """
 
 from __future__ import annotations
@@ -140,6 +145,29 @@ def bench_attention(torch, dev, backend, steps, warmup, cache, inputs):
     if not bool(torch.isfinite(out).all()):
         raise RuntimeError(f"{backend} attention produced non-finite output")
     return wall_ms, dev_ms, comps
+
+
+def bench_reference_sdpa(torch, dev, steps, warmup, cache, inputs):
+    """The reference's serial backend on this GPU, same inputs: per layer call it
+    concatenates the token-major history and the chunk's K/V into dense
+    tensors (attention_hook.py:56-97) and runs torch SDPA (:100-115).  Operands
+    are made head-major contiguous (the reference passes transposed views; the
+    extra copies are under 1% of the call) and SDPA is held to its fused
+    flash / memory-efficient kernels.  Returns ms per call."""
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    hist = cache.history(LAYER)
+    q = inputs["query"].transpose(0, 1).unsqueeze(0).contiguous()
+
+    def call():
+        k = torch.cat([hist.key, inputs["key"]]).transpose(0, 1).unsqueeze(0).contiguous()
+        v = torch.cat([hist.value, inputs["value"]]).transpose(0, 1).unsqueeze(0).contiguous()
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            return F.scaled_dot_product_attention(q, k, v, scale=D ** -0.5)
+
+    _, dev_ms = time_steps(torch, call, steps, warmup)
+    return dev_ms
 
 
 def bench_w8a8(torch, dev, steps, warmup):
@@ -282,6 +310,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-reference-gpu", action="store_true",
+                    help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
     ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "copy"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -369,6 +399,16 @@ def main() -> int:
             "kernel_ms": round(attn_ms, 4),
         }
         _log(f"bf16: {wall_ms:.3f} ms/step (device {dev_ms:.3f}), kernel {attn_ms:.3f} ms = {achieved:.1f} TFLOPS")
+        if not args.no_reference_gpu:
+            ref_ms = bench_reference_sdpa(torch, dev, min(args.steps, 5), 1, cache, inputs)
+            result["reference_backend_gpu"] = {
+                "kind": "the reference's serial backend (dense K/V concatenation + torch SDPA, flash / "
+                        "memory-efficient kernels) on this GPU, same inputs, bf16",
+                "ms_per_layer_call": round(ref_ms, 3),
+                "tflops": round(ATTN_FLOPS / (ref_ms * 1e-3) / 1e12, 1),
+                "speedup_of_value": round(ref_ms / wall_ms, 2),
+            }
+            _log(f"reference backend on this GPU: {ref_ms:.3f} ms per layer call")
     if args.workload in ("all", "i8qk"):
         wall_ms, dev_ms, comps = bench_attention(torch, dev, "sage_attn", args.steps, args.warmup, cache, inputs)
         tflops = ATTN_FLOPS / (wall_ms * 1e-3) / 1e12
