@@ -337,6 +337,27 @@ int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m,
                      int32_t n, int32_t k, int64_t lda, int64_t ldb,
                      int64_t ldo, void *stream);
 
+/*
+ * No counterpart in the reference (the caller-provided scratch of the two
+ * GEMMs above).  When the 256 x 256 tiles leave a last round that fills at
+ * most half of the CUs (or fill less than half in all), that round's tiles
+ * are split along k into up to CUs / tiles parts of at least 4 k-stages;
+ * the parts' int32 partial tiles go to `workspace` and a second pass adds
+ * them (exactly) and applies the same epilogue, so results are bit-identical
+ * to the unsplit GEMM.  tmhd_gemm_split_workspace_bytes gives the bytes this
+ * needs on the current device for the shape (0: no split); with a smaller or
+ * null workspace the _ws calls run unsplit.  Partial tiles of calls that
+ * overlap on one workspace race.
+ */
+int64_t tmhd_gemm_split_workspace_bytes(int32_t m, int32_t n, int32_t k);
+int tmhd_gemm_w8a8_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
+                      const float *b_scale, const void *bias, int32_t m, int32_t n, int32_t k,
+                      int64_t lda, int64_t ldb, int64_t ldo, void *workspace,
+                      int64_t workspace_bytes, void *stream);
+int tmhd_gemm_i8_i32_ws(int32_t *out, const int8_t *a, const int8_t *b, int32_t m, int32_t n,
+                        int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *workspace,
+                        int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -931,19 +931,6 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const KArgs a) {
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
-// Compute units of the current device (cached per device).
-int device_cus() {
-  static int cus[64] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
-
 int64_t split_slot_bytes(int D) { return (int64_t)kBM * (D + 1) * 4; }
 
 // Key ranges per remaining item: as many as fit the CUs the whole items leave

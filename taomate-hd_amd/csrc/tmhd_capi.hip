@@ -18,6 +18,18 @@ int set_error(int status, const char *fmt, ...) {
   return status;
 }
 
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
 int check_launch(const char *what) {
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return set_error(TMHD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));

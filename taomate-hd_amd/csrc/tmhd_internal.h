@@ -20,6 +20,8 @@ using bf16x8 = __bf16 __attribute__((ext_vector_type(8)));
 int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 // Checks hipGetLastError() after a launch; records it on failure.
 int check_launch(const char *what);
+// Compute units of the current device (cached per device; 0 if unknown).
+int device_cus();
 
 // bf16 bits -> fp32 (exact).
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {

@@ -6,6 +6,8 @@
 
 #include <type_traits>
 
+#include <algorithm>
+
 #include "tmhd_internal.h"
 
 namespace tmhd {
@@ -148,7 +150,33 @@ struct GArgs {
   int32_t tm_count, tn_count;
   int32_t vec_ok;  // bs 16-byte and bias 8-byte aligned: vector loads of 4 columns
   int32_t st_ok;   // bf16 output rows 16-byte aligned: staged 16-byte stores
+  // K split of the last, partial round (one-wave-per-SIMD kernel): tiles
+  // [0, full) are whole; block t * nsplit + p of the split launch is k-range p
+  // of tile full + t, whose int32 partial tile goes to ws (merged afterwards)
+  int32_t full, nsplit;
+  int32_t *ws;
 };
+
+// Tile (tm, tn) of logical tile L: 8 row tiles share each column sweep (L2 reuse).
+__device__ __forceinline__ void grouped_tile(int L, int tm_count, int tn_count, int &tm, int &tn) {
+  constexpr int GROUP = 8;
+  const int per_group = GROUP * tn_count;
+  const int first_tm = (L / per_group) * GROUP;
+  const int gsize = min(tm_count - first_tm, GROUP);
+  tm = first_tm + (L % per_group) % gsize;
+  tn = (L % per_group) / gsize;
+}
+
+// The dequantisation epilogue of one accumulator, the same operations in the
+// same order as the GEMM's own epilogue: (float)acc * b_scale * a_scale (+ bias).
+__device__ __forceinline__ uint16_t dequant_bf16(int32_t acc, float bs, float as, bool has_bias, uint32_t bias_bits) {
+#pragma clang fp contract(off)
+  float t = (float)acc;
+  t = t * bs;
+  t = t * as;
+  if (has_bias) t = t + bf16_bits_to_f32(bias_bits);
+  return f32_to_bf16_bits(t);
+}
 
 __device__ __forceinline__ int xcd_logical_id(int b, int G) {
   const int xcd = b & 7, pos = b >> 3, per = G >> 3, rem = G & 7;
@@ -324,7 +352,7 @@ __device__ __forceinline__ void hload_lds16(const void *base, uint32_t off, uint
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
-template <bool RAW>
+template <bool RAW, bool SPLIT>
 __global__ void __launch_bounds__(HWAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma clang fp contract(off)
@@ -333,15 +361,22 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w >> 1, wn = w & 1;  // wave tile: a rows [wm*128, +128), b rows [wn*128, +128)
-  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
-  constexpr int GROUP = 8;  // 8 row tiles share each column sweep (L2 reuse)
-  const int per_group = GROUP * ga.tn_count;
-  const int grp = L / per_group;
-  const int first_tm = grp * GROUP;
-  const int gsize = min(ga.tm_count - first_tm, GROUP);
-  const int tm = first_tm + (L % per_group) % gsize;
-  const int tn = (L % per_group) / gsize;
+  // whole tile, or (SPLIT) k-stage range [s_begin, s_end) of a tile of the split round
+  const int nst_all = ga.k / HKS;
+  int L, part = 0, s_begin = 0, s_end = nst_all;
+  if constexpr (SPLIT) {
+    const int item = blockIdx.x / ga.nsplit;
+    part = blockIdx.x - item * ga.nsplit;
+    L = ga.full + item;
+    s_begin = nst_all * part / ga.nsplit;
+    s_end = nst_all * (part + 1) / ga.nsplit;
+  } else {
+    L = xcd_logical_id(blockIdx.x, gridDim.x);
+  }
+  int tm, tn;
+  grouped_tile(L, ga.tm_count, ga.tn_count, tm, tn);
   const int m0 = tm * HBM_, n0 = tn * HBN;
+  const int8_t *abase = ga.a + (int64_t)s_begin * HKS, *bbase = ga.b + (int64_t)s_begin * HKS;
 
   // loads: 16 blocks of 1 KiB (16 rows of 64 B) per operand and stage; wave w
   // loads blocks w, w + 4, w + 8, w + 12 of each.  Lane: row 16 blk + lane / 4,
@@ -358,9 +393,9 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   auto load_one = [&](int n, int kt, uint32_t stage) {
     const int i = n & 3;
     if (n < 4)
-      hload_lds16(ga.a + (int64_t)kt * HKS, aoff[i], stage + (w + 4 * i) * 1024);
+      hload_lds16(abase + (int64_t)kt * HKS, aoff[i], stage + (w + 4 * i) * 1024);
     else
-      hload_lds16(ga.b + (int64_t)kt * HKS, boff[i], stage + HSIDE + (w + 4 * i) * 1024);
+      hload_lds16(bbase + (int64_t)kt * HKS, boff[i], stage + HSIDE + (w + 4 * i) * 1024);
   };
   // operand read offsets (k-step ks): row base + swizzled chunk 2 ks + g
   const int x = (lr >> 2) & 3;
@@ -386,7 +421,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int nst = ga.k / HKS;
+  const int nst = s_end - s_begin;  // >= 1
   // prologue: stages 0..4 in flight (past the last stage the loads repeat it,
   // into slots that are never read); stage 0 landed, then its k-step 0 operands
 #pragma unroll
@@ -438,6 +473,24 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   if (s + 3 < nst) stage(std::integral_constant<int, 3>{}, s + 3);
   // every wave drains its loads before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0x0f70);
+
+  if constexpr (SPLIT) {
+    // k-range of a split tile: the raw 256 x 256 int32 partial, row-major
+    int32_t *wp = ga.ws + ((int64_t)(L - ga.full) * ga.nsplit + part) * (HBM_ * HBN);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int m = wm * 128 + j * 32 + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int n = wn * 128 + i * 32 + 8 * u + 4 * g;
+          *(i32x4 *)(wp + m * HBN + n) =
+              i32x4{acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
+        }
+    }
+    return;
+  }
 
   // epilogue: lane holds m = m-block base + lr; n = n-block base + 8u + 4g + (0..3).
   // The column scales and bias of the lane's 16 n-groups are loaded once.
@@ -558,9 +611,66 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   }
 }
 
+// Merge of the K-split tiles: the sum of each tile's nsplit int32 partials
+// (exact), then the GEMM's epilogue.  Block: 4 rows of one tile, 4 columns
+// per thread.
+template <bool RAW>
+__global__ void __launch_bounds__(256) gemm_split_merge_kernel(const GArgs ga) {
+  const int item = blockIdx.x / (HBM_ / 4);
+  const int r = (blockIdx.x % (HBM_ / 4)) * 4 + (threadIdx.x >> 6);
+  const int c = (threadIdx.x & 63) * 4;
+  int tm, tn;
+  grouped_tile(ga.full + item, ga.tm_count, ga.tn_count, tm, tn);
+  const int m = tm * HBM_ + r, n = tn * HBN + c;
+  if (m >= ga.m || n >= ga.n) return;
+  const int32_t *wp = ga.ws + (int64_t)item * ga.nsplit * (HBM_ * HBN) + r * HBN + c;
+  i32x4 acc = *(const i32x4 *)wp;
+  for (int p = 1; p < ga.nsplit; ++p) acc += *(const i32x4 *)(wp + (int64_t)p * (HBM_ * HBN));
+  if constexpr (RAW) {
+    int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
+    if (n + 3 < ga.n)
+      *(i32x4 *)op = acc;
+    else
+      for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[e];
+  } else {
+    const float asm_ = ga.as[m];
+    uint16_t vals[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int nn = min(n + e, ga.n - 1);
+      vals[e] = dequant_bf16(acc[e], ga.bs[nn], asm_, ga.bias != nullptr, ga.bias ? ga.bias[nn] : 0u);
+    }
+    uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+    if (n + 3 < ga.n)
+      *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                           (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+    else
+      for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
+  }
+}
+
+// K split of the last, partial round of 256 x 256 tiles (all tiles when they
+// fill less than half the CUs): its tiles' k-stages are dealt to S parts, S
+// up to CUs / tiles and at least 4 stages per part, so that the round fills
+// the CUs; the partials are merged by gemm_split_merge_kernel.
+void gemm_split_plan(int32_t m, int32_t n, int32_t k, int &tail, int &parts) {
+  tail = 0, parts = 1;
+  const int cus = device_cus();
+  if (cus <= 0 || m <= 0 || n <= 0 || k <= 0 || k % HKS) return;
+  const int64_t tiles = (int64_t)((m + HBM_ - 1) / HBM_) * ((n + HBN - 1) / HBN);
+  const int64_t t = tiles % cus;
+  if (t == 0 || 2 * t > cus) return;
+  const int64_t s = std::min<int64_t>(cus / t, (k / HKS) / 4);
+  if (s < 2) return;
+  tail = (int)t, parts = (int)s;
+}
+
+int64_t gemm_split_bytes(int tail, int parts) { return (int64_t)tail * parts * HBM_ * HBN * 4; }
+
 template <bool RAW>
 int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, const float *bs, const void *bias,
-                int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *stream) {
+                int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *ws, int64_t ws_bytes,
+                void *stream) {
   const char *what = RAW ? "tmhd_gemm_i8_i32" : "tmhd_gemm_w8a8";
   if (m < 0 || n <= 0 || k <= 0) return set_error(TMHD_ERR_INVALID, "%s: m %d n %d k %d", what, m, n, k);
   if (k % GBK) return set_error(TMHD_ERR_UNSUPPORTED, "%s: k %d must be a multiple of %d", what, k, GBK);
@@ -568,18 +678,33 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
   if (((uintptr_t)a % 16) || ((uintptr_t)b % 16) || lda % 16 || ldb % 16 || lda < k || ldb < k || ldo < n)
     return set_error(TMHD_ERR_INVALID, "%s: operands must be 16-byte aligned rows with stride >= k", what);
   if (m == 0) return TMHD_OK;
+  const int64_t tiles = (int64_t)((m + GBM - 1) / GBM) * ((n + GBN - 1) / GBN);
   GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + GBM - 1) / GBM, (n + GBN - 1) / GBN,
            (int32_t)(((uintptr_t)bs % 16) == 0 && ((uintptr_t)bias % 8) == 0),
-           (int32_t)(!RAW && ((uintptr_t)out % 16) == 0 && ldo % 8 == 0)};
-  const int64_t grid = (int64_t)ga.tm_count * ga.tn_count;
+           (int32_t)(!RAW && ((uintptr_t)out % 16) == 0 && ldo % 8 == 0), (int32_t)tiles, 1, nullptr};
+  const int64_t grid = tiles;
   // the one-wave-per-SIMD kernel takes 32-bit row offsets
   const bool wide = (int64_t)(m - 1) * lda + k < ((int64_t)1 << 32) &&
                     (int64_t)(n - 1) * ldb + k < ((int64_t)1 << 32);
-  if (wide)
-    hipLaunchKernelGGL(gemm_i8_wave128_kernel<RAW>, dim3((unsigned)grid), dim3(HWAVES * 64), 0, (hipStream_t)stream,
-                       ga);
-  else
+  if (wide) {
+    int tail = 0, parts = 1;
+    gemm_split_plan(m, n, k, tail, parts);
+    if (parts > 1 && ws && ((uintptr_t)ws % 16) == 0 && ws_bytes >= gemm_split_bytes(tail, parts)) {
+      ga.full = (int32_t)(tiles - tail);
+      ga.nsplit = parts;
+      ga.ws = (int32_t *)ws;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    if (ga.full > 0)
+      hipLaunchKernelGGL((gemm_i8_wave128_kernel<RAW, false>), dim3((unsigned)ga.full), dim3(HWAVES * 64), 0, s, ga);
+    if (ga.nsplit > 1) {
+      hipLaunchKernelGGL((gemm_i8_wave128_kernel<false, true>), dim3((unsigned)(tail * parts)), dim3(HWAVES * 64), 0,
+                         s, ga);
+      hipLaunchKernelGGL(gemm_split_merge_kernel<RAW>, dim3((unsigned)(tail * (HBM_ / 4))), dim3(256), 0, s, ga);
+    }
+  } else {
     hipLaunchKernelGGL(gemm_i8_kernel<RAW>, dim3((unsigned)grid), dim3(GWAVES * 64), 0, (hipStream_t)stream, ga);
+  }
   return check_launch(what);
 }
 
@@ -598,10 +723,30 @@ extern "C" int tmhd_weight_quant_i8(int8_t *q, float *scale, const void *w, int3
 extern "C" int tmhd_gemm_w8a8(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
                               const float *b_scale, const void *bias, int32_t m, int32_t n, int32_t k, int64_t lda,
                               int64_t ldb, int64_t ldo, void *stream) {
-  return tmhd::launch_gemm<false>(out, a, b, a_scale, b_scale, bias, m, n, k, lda, ldb, ldo, stream);
+  return tmhd::launch_gemm<false>(out, a, b, a_scale, b_scale, bias, m, n, k, lda, ldb, ldo, nullptr, 0, stream);
 }
 
 extern "C" int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m, int32_t n, int32_t k,
                                 int64_t lda, int64_t ldb, int64_t ldo, void *stream) {
-  return tmhd::launch_gemm<true>(out, a, b, nullptr, nullptr, nullptr, m, n, k, lda, ldb, ldo, stream);
+  return tmhd::launch_gemm<true>(out, a, b, nullptr, nullptr, nullptr, m, n, k, lda, ldb, ldo, nullptr, 0, stream);
+}
+
+extern "C" int64_t tmhd_gemm_split_workspace_bytes(int32_t m, int32_t n, int32_t k) {
+  int tail = 0, parts = 1;
+  tmhd::gemm_split_plan(m, n, k, tail, parts);
+  return parts > 1 ? tmhd::gemm_split_bytes(tail, parts) : 0;
+}
+
+extern "C" int tmhd_gemm_w8a8_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
+                                 const float *b_scale, const void *bias, int32_t m, int32_t n, int32_t k, int64_t lda,
+                                 int64_t ldb, int64_t ldo, void *workspace, int64_t workspace_bytes, void *stream) {
+  return tmhd::launch_gemm<false>(out, a, b, a_scale, b_scale, bias, m, n, k, lda, ldb, ldo, workspace,
+                                  workspace_bytes, stream);
+}
+
+extern "C" int tmhd_gemm_i8_i32_ws(int32_t *out, const int8_t *a, const int8_t *b, int32_t m, int32_t n, int32_t k,
+                                   int64_t lda, int64_t ldb, int64_t ldo, void *workspace, int64_t workspace_bytes,
+                                   void *stream) {
+  return tmhd::launch_gemm<true>(out, a, b, nullptr, nullptr, nullptr, m, n, k, lda, ldb, ldo, workspace,
+                                 workspace_bytes, stream);
 }

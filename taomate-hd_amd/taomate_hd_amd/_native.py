@@ -144,6 +144,17 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         c_int,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_void_p],
     ),
+    "tmhd_gemm_split_workspace_bytes": (c_int64, [c_int32, c_int32, c_int32]),
+    "tmhd_gemm_w8a8_ws": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64,
+         c_int64, c_void_p, c_int64, c_void_p],
+    ),
+    "tmhd_gemm_i8_i32_ws": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,
+         c_void_p],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

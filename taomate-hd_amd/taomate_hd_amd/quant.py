@@ -107,6 +107,23 @@ def _gemm_operands(torch: Any, a: Any, b: Any) -> tuple[int, int, int, int, int]
     return m, n, k, a.stride(0), b.stride(1)
 
 
+_SPLIT_WS: dict[str, Any] = {}
+
+
+def _split_workspace(torch: Any, device: Any, m: int, n: int, k: int) -> tuple[int | None, int]:
+    """Grow-only per-device scratch for the K split of the GEMM's last round
+    (int32 partial tiles; reused by work queued later on the same stream)."""
+    need = int(_native.load().tmhd_gemm_split_workspace_bytes(m, n, k))
+    if need <= 0:
+        return None, 0
+    key = str(device)
+    ws = _SPLIT_WS.get(key)
+    if ws is None or int(ws.numel()) < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+        _SPLIT_WS[key] = ws
+    return _native.ptr(ws), int(ws.numel())
+
+
 def cutlass_scaled_mm_out(out: Any, a: Any, b: Any, scale_a: Any, scale_b: Any, bias: Any | None = None) -> None:
     """out = bf16(float(a @ b) * scale_b[n] * scale_a[m] (+ bias[n])), int32 accumulate."""
     torch = _torch()
@@ -127,11 +144,12 @@ def cutlass_scaled_mm_out(out: Any, a: Any, b: Any, scale_a: Any, scale_b: Any, 
             raise ValueError("bias must be a bf16 vector of N values")
         bias = bias.contiguous()
         bias_ptr = _native.ptr(bias)
-    status = _native.load().tmhd_gemm_w8a8(
+    ws, ws_bytes = _split_workspace(torch, a.device, m, n, k)
+    status = _native.load().tmhd_gemm_w8a8_ws(
         _native.ptr(out), _native.ptr(a), _native.ptr(b), _native.ptr(sa), _native.ptr(sb), bias_ptr,
-        m, n, k, lda, ldb, out.stride(0), _native.stream_ptr(torch, a.device),
+        m, n, k, lda, ldb, out.stride(0), ws, ws_bytes, _native.stream_ptr(torch, a.device),
     )
-    _native.check(status, "tmhd_gemm_w8a8")
+    _native.check(status, "tmhd_gemm_w8a8_ws")
 
 
 def cutlass_scaled_mm(a: Any, b: Any, scale_a: Any, scale_b: Any, out_dtype: Any = None, bias: Any | None = None):
@@ -149,8 +167,10 @@ def int8_mm_i32(a: Any, b: Any) -> Any:
     torch = _torch()
     m, n, k, lda, ldb = _gemm_operands(torch, a, b)
     out = torch.empty((m, n), dtype=torch.int32, device=a.device)
-    status = _native.load().tmhd_gemm_i8_i32(
-        _native.ptr(out), _native.ptr(a), _native.ptr(b), m, n, k, lda, ldb, n, _native.stream_ptr(torch, a.device)
+    ws, ws_bytes = _split_workspace(torch, a.device, m, n, k)
+    status = _native.load().tmhd_gemm_i8_i32_ws(
+        _native.ptr(out), _native.ptr(a), _native.ptr(b), m, n, k, lda, ldb, n, ws, ws_bytes,
+        _native.stream_ptr(torch, a.device)
     )
-    _native.check(status, "tmhd_gemm_i8_i32")
+    _native.check(status, "tmhd_gemm_i8_i32_ws")
     return out

@@ -264,3 +264,33 @@ def test_gemm_accumulators_and_epilogue_bit_exact(torch_mod, dev, m, n, k):
     )
     torch.cuda.synchronize()
     assert np.array_equal(bf16.from_torch(out2), oq.scaled_mm_epilogue(want, sa, sb, None))
+
+
+def test_gemm_split_round_equals_unsplit(torch_mod, dev):
+    # 15 x 18 = 270 tiles: on 256 CUs one whole round plus a 14-tile round that
+    # is split along k; the split + merge must equal the unsplit GEMM bit for bit
+    torch = torch_mod
+    from taomate_hd_amd import _native, quant
+
+    m, n, k = 15 * 256 - 100, 18 * 256 - 30, 1024
+    rng = np.random.default_rng(5)
+    ad = torch.from_numpy(rng.integers(-128, 128, size=(m, k), dtype=np.int8)).to(dev)
+    wd = torch.from_numpy(rng.integers(-127, 128, size=(n, k), dtype=np.int8)).to(dev)
+    lib = _native.load()
+    assert lib.tmhd_gemm_split_workspace_bytes(m, n, k) > 0
+    stream = _native.stream_ptr(torch, dev)
+    plain = torch.empty((m, n), dtype=torch.int32, device=dev)
+    _native.check(lib.tmhd_gemm_i8_i32(_native.ptr(plain), _native.ptr(ad), _native.ptr(wd), m, n, k, k, k, n, stream),
+                  "tmhd_gemm_i8_i32")
+    split = quant.int8_mm_i32(ad, wd.t())
+    torch.cuda.synchronize()
+    assert torch.equal(plain, split)
+    sa = torch.from_numpy(rng.random(m, dtype=np.float32) * 0.05 + 1e-3).to(dev)
+    sb = torch.from_numpy(rng.random(n, dtype=np.float32) * 0.01 + 1e-4).to(dev)
+    bias = to_dev(randn_bf16((n,), 61, std=0.02), dev)
+    ref = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    _native.check(lib.tmhd_gemm_w8a8(_native.ptr(ref), _native.ptr(ad), _native.ptr(wd), _native.ptr(sa),
+                                     _native.ptr(sb), _native.ptr(bias), m, n, k, k, k, n, stream), "tmhd_gemm_w8a8")
+    out = quant.cutlass_scaled_mm(ad, wd.t(), sa.view(m, 1), sb.view(1, n), torch.bfloat16, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
