@@ -168,14 +168,22 @@ __device__ __forceinline__ void grouped_tile(int L, int tm_count, int tn_count, 
 }
 
 // The dequantisation epilogue of one accumulator, the same operations in the
-// same order as the GEMM's own epilogue: (float)acc * b_scale * a_scale (+ bias).
-__device__ __forceinline__ uint16_t dequant_bf16(int32_t acc, float bs, float as, bool has_bias, uint32_t bias_bits) {
+// same order as the GEMM's own epilogue: (float)acc * b_scale * a_scale (+ bias);
+// rounded to bf16 by bf16_quad.
+__device__ __forceinline__ float dequant_f32(int32_t acc, float bs, float as, bool has_bias, uint32_t bias_bits) {
 #pragma clang fp contract(off)
   float t = (float)acc;
   t = t * bs;
   t = t * as;
   if (has_bias) t = t + bf16_bits_to_f32(bias_bits);
-  return f32_to_bf16_bits(t);
+  return t;
+}
+
+// Four floats -> bf16 with gfx950's conversion (round to nearest even, two
+// per instruction; the same bits as f32_to_bf16_bits for every non-NaN value).
+__device__ __forceinline__ void bf16_quad(const float (&t)[4], uint16_t (&v)[4]) {
+  const uint32_t p01 = pack_bf16_rne(t[0], t[1]), p23 = pack_bf16_rne(t[2], t[3]);
+  v[0] = (uint16_t)p01, v[1] = (uint16_t)(p01 >> 16), v[2] = (uint16_t)p23, v[3] = (uint16_t)(p23 >> 16);
 }
 
 __device__ __forceinline__ int xcd_logical_id(int b, int G) {
@@ -307,6 +315,7 @@ gemm_i8_kernel(const GArgs ga) {
         } else {
           uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
           uint16_t vals[4];
+          float tv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int nn = min(n + e, ga.n - 1);
@@ -314,8 +323,9 @@ gemm_i8_kernel(const GArgs ga) {
             t = t * ga.bs[nn];
             t = t * asm_;
             if (ga.bias) t = t + bf16_bits_to_f32(ga.bias[nn]);
-            vals[e] = f32_to_bf16_bits(t);
+            tv[e] = t;
           }
+          bf16_quad(tv, vals);
           if (n + 3 < ga.n) {
             *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
                                  (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
@@ -534,6 +544,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             uint16_t vals[4];
+            float tv[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               float t = (float)acc[i][j][4 * u + e];
@@ -543,8 +554,9 @@ gemm_i8_wave128_kernel(const GArgs ga) {
                 const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
                 t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
               }
-              vals[e] = f32_to_bf16_bits(t);
+              tv[e] = t;
             }
+            bf16_quad(tv, vals);
             *(i32x2 *)(smem + wt + (j * 32 + lr) * ROWB + (i * 32 + 8 * u + 4 * g) * 2) =
                 i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
                       (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
@@ -588,6 +600,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
         } else {
           uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
           uint16_t vals[4];
+          float tv[4];
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float t = (float)acc[i][j][4 * u + e];
@@ -597,8 +610,9 @@ gemm_i8_wave128_kernel(const GArgs ga) {
               const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
               t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
             }
-            vals[e] = f32_to_bf16_bits(t);
+            tv[e] = t;
           }
+          bf16_quad(tv, vals);
           if (n + 3 < ga.n) {
             *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
                                  (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
@@ -635,11 +649,13 @@ __global__ void __launch_bounds__(256) gemm_split_merge_kernel(const GArgs ga) {
   } else {
     const float asm_ = ga.as[m];
     uint16_t vals[4];
+    float tv[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int nn = min(n + e, ga.n - 1);
-      vals[e] = dequant_bf16(acc[e], ga.bs[nn], asm_, ga.bias != nullptr, ga.bias ? ga.bias[nn] : 0u);
+      tv[e] = dequant_f32(acc[e], ga.bs[nn], asm_, ga.bias != nullptr, ga.bias ? ga.bias[nn] : 0u);
     }
+    bf16_quad(tv, vals);
     uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
     if (n + 3 < ga.n)
       *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
