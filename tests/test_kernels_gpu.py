@@ -294,3 +294,49 @@ def test_gemm_split_round_equals_unsplit(torch_mod, dev):
     out = quant.cutlass_scaled_mm(ad, wd.t(), sa.view(m, 1), sb.view(1, n), torch.bfloat16, bias)
     torch.cuda.synchronize()
     assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+
+@pytest.mark.parametrize("backend", ["bf16", "i8qk"])
+@pytest.mark.parametrize(
+    "lq,splits",
+    [
+        (4836, [1560, 4836, 4836, 4836]),  # 480p stage: Lkv 16,068 (anchor + two history chunks + self)
+        (12252, [4032, 12252, 12252, 12252]),  # 768p stage: Lkv 40,788
+    ],
+)
+def test_full_size_stage_shapes_on_sampled_rows(torch_mod, dev, backend, lq, splits):
+    """The stage shapes at full size (40 heads, head_dim 128): the whole
+    attention runs; 64 query rows of 3 heads are checked against the fp64
+    oracle over every key (BF16 gate, or the INT8-QK cosine gate)."""
+    torch = torch_mod
+    from taomate_hd_amd import KVSlot, segment_attention
+
+    H, D = 40, 128
+    n = sum(splits)
+    gen = torch.Generator(device=dev).manual_seed(lq)
+    q = torch.randn(lq, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    off = 0.5 * torch.randn(H, D, generator=gen, device=dev)
+    k = (torch.randn(n, H, D, generator=gen, device=dev) + off).to(torch.bfloat16)
+    v = torch.randn(n, H, D, generator=gen, device=dev).to(torch.bfloat16)
+    views, row = [], 0
+    for c in splits:
+        s = KVSlot(torch, heads=H, head_dim=D, capacity=c, device=dev)
+        s.pack(k, v, row0=row, count=c)
+        views.append(s.view())
+        row += c
+    out = segment_attention(torch, q, views, scale=D ** -0.5, backend=backend)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(lq)
+    rows = np.unique(np.concatenate([[0, lq - 1], rng.integers(0, lq, 62)]))
+    heads = [0, 17, 39]
+    qs = bf16.from_torch(q[torch.tensor(rows, device=dev)][:, heads].contiguous())
+    ks = bf16.from_torch(k[:, heads].contiguous())
+    vs = bf16.from_torch(v[:, heads].contiguous())
+    got = bf16.from_torch(out[torch.tensor(rows, device=dev)][:, heads].contiguous())
+    want = oatt.attention_fp64(qs, ks, vs, D ** -0.5)
+    assert np.all(np.isfinite(got))
+    if backend == "bf16":
+        mx, mean = err_stats(got, want)
+        assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+    else:
+        assert oatt.cosine(got, want) >= I8_COSINE
