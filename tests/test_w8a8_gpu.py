@@ -67,3 +67,28 @@ def test_registered_torch_ops(torch_mod, dev):
     ops.cutlass_scaled_mm(out, q, qw.t(), s, sw.t(), None)
     torch.cuda.synchronize()
     assert np.array_equal(bf16.from_torch(out), _expected(x, w))
+
+
+def test_w8a8_projection_full_size_sampled_rows(torch_mod, dev):
+    """The 768p projection at full size (12,252 x 5,120 -> 13,824, bf16 bias):
+    the whole GEMM runs (whole tiles, the k-split last round and its merge);
+    24 rows, spread over every row tile, are checked bit for bit against the
+    oracle (token quantization is per row, so sampled rows stand alone)."""
+    torch = torch_mod
+    from taomate_hd_amd import cutlass_w8a8_linear, quantize_cutlass_w8a8_weight
+
+    m, k, n = 12252, 5120, 13824
+    gen = torch.Generator(device=dev).manual_seed(3)
+    xd = torch.randn(m, k, generator=gen, device=dev)
+    xd[:, 7] *= 20.0  # an outlier channel
+    xd = xd.to(torch.bfloat16)
+    wd = (0.02 * torch.randn(n, k, generator=gen, device=dev)).to(torch.bfloat16)
+    bd = (0.02 * torch.randn(n, generator=gen, device=dev)).to(torch.bfloat16)
+    qw, sw = quantize_cutlass_w8a8_weight(torch, wd)
+    out = cutlass_w8a8_linear(torch, xd, qw, sw, bias=bd)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([[0, m - 1], np.arange(12, m, 512)]))[:24]
+    x = bf16.from_torch(xd[torch.tensor(rows, device=dev)].contiguous())
+    want = _expected(x, bf16.from_torch(wd), bf16.from_torch(bd))
+    got = bf16.from_torch(out[torch.tensor(rows, device=dev)].contiguous())
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
