@@ -46,7 +46,9 @@ def _weight(torch: Any, weight: Any, cols: int) -> Any:
     return weight.reshape(-1).contiguous()
 
 
-def _index(torch: Any, indices: Any, rows: int, message: str | None) -> Any:
+def _index(torch: Any, indices: Any, rows: int, message: str | None, device: Any) -> Any:
+    if not torch.is_tensor(indices) or indices.device != device:
+        raise ValueError("SOL table indices must be a tensor on the GPU of the rows")
     index = indices.reshape(-1).to(dtype=torch.int64).contiguous()
     if message is not None and int(index.numel()) != rows:
         raise ValueError(message)
@@ -81,7 +83,7 @@ def fused_rms_norm_modulate(value: Any, weight: Any, scale: Any, shift: Any, ind
     shape = value.shape
     flat = _rows(torch, value, "value")
     rows, cols = int(flat.shape[0]), int(flat.shape[1])
-    index = _index(torch, indices, rows, "SOL RMSNorm/AdaLN indices do not cover every row")
+    index = _index(torch, indices, rows, "SOL RMSNorm/AdaLN indices do not cover every row", flat.device)
     w = _weight(torch, weight, cols)
     scale, shift = _table(torch, scale, "scale", cols), _table(torch, shift, "shift", cols)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device)
@@ -104,7 +106,7 @@ def fused_residual_gate_rms_norm_modulate(residual: Any, branch: Any, gate: Any,
     br = _rows(torch, branch.reshape(-1, cols), "branch")
     if int(br.shape[0]) != rows:
         raise ValueError("SOL residual and branch rows differ")
-    index = _index(torch, indices, rows, "SOL residual/AdaLN indices do not cover every row")
+    index = _index(torch, indices, rows, "SOL residual/AdaLN indices do not cover every row", res.device)
     w = _weight(torch, weight, cols)
     gate, scale, shift = (_table(torch, t, n, cols) for t, n in ((gate, "gate"), (scale, "scale"), (shift, "shift")))
     hidden = torch.empty((rows, cols), dtype=torch.bfloat16, device=res.device)
@@ -124,7 +126,7 @@ def fused_modulate(value: Any, shift: Any, scale: Any, indices: Any) -> Any:
     shape = value.shape
     flat = _rows(torch, value, "value")
     rows, cols = int(flat.shape[0]), int(flat.shape[1])
-    index = _index(torch, indices, rows, None)
+    index = _index(torch, indices, rows, None, flat.device)
     scale, shift = _table(torch, scale, "scale", cols), _table(torch, shift, "shift", cols)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device)
     _run(_native.load().tmhd_modulate(
@@ -144,7 +146,7 @@ def fused_gate_add(residual: Any, gate: Any, branch: Any, indices: Any) -> Any:
     br = _rows(torch, branch.reshape(-1, cols), "branch")
     if int(br.shape[0]) != rows:
         raise ValueError("SOL residual and branch rows differ")
-    index = _index(torch, indices, rows, None)
+    index = _index(torch, indices, rows, None, res.device)
     gate = _table(torch, gate, "gate", cols)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=res.device)
     _run(_native.load().tmhd_gate_add(

@@ -21,11 +21,13 @@ from . import _native
 from .attention import segment_attention
 from .slots import KV_TILE, SlotPool, SlotView, round_up
 
-_POOLS: dict[tuple[str, int, int], SlotPool] = {}
+_POOLS: dict[tuple[str, int, int, int], SlotPool] = {}
 
 
 def _pool(torch: Any, device: Any, heads: int, head_dim: int) -> SlotPool:
-    key = (str(torch.device(device)), int(heads), int(head_dim))
+    """Slots per (device, stream, shape): a released slot is reused only by
+    work queued after its readers on the same stream."""
+    key = (str(torch.device(device)), _native.stream_ptr(torch, device), int(heads), int(head_dim))
     if key not in _POOLS:
         _POOLS[key] = SlotPool(torch, heads=heads, head_dim=head_dim, device=device)
     return _POOLS[key]
@@ -77,5 +79,5 @@ def packed_sdpa(q: Any, k: Any, v: Any, *, cu_seqlens: Any, cu_seqlens_host: tup
             segment_attention(torch, q, [SlotView(slot, stop - start, dst)], scale=float(scale), backend="bf16",
                               q_row0=start, lq=stop - start, out=out, o_row0=start)
     finally:
-        pool.release(slot)  # reused only by work queued after these launches on the same stream
+        pool.release(slot)
     return out

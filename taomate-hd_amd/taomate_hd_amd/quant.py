@@ -107,16 +107,17 @@ def _gemm_operands(torch: Any, a: Any, b: Any) -> tuple[int, int, int, int, int]
     return m, n, k, a.stride(0), b.stride(1)
 
 
-_SPLIT_WS: dict[str, Any] = {}
+_SPLIT_WS: dict[tuple[str, int], Any] = {}
 
 
 def _split_workspace(torch: Any, device: Any, m: int, n: int, k: int) -> tuple[int | None, int]:
-    """Grow-only per-device scratch for the K split of the GEMM's last round
-    (int32 partial tiles; reused by work queued later on the same stream)."""
+    """Grow-only scratch for the K split of the GEMM's last round (int32
+    partial tiles), one per (device, stream): calls on one stream are
+    ordered, so they share it."""
     need = int(_native.load().tmhd_gemm_split_workspace_bytes(m, n, k))
     if need <= 0:
         return None, 0
-    key = str(device)
+    key = (str(device), _native.stream_ptr(torch, device))
     ws = _SPLIT_WS.get(key)
     if ws is None or int(ws.numel()) < need:
         ws = torch.empty(need, dtype=torch.uint8, device=device)

@@ -77,6 +77,8 @@ def test_row_ops_index_clamp_and_checks(torch_mod, dev):
     with pytest.raises(ValueError, match="indices do not cover every row"):
         fused_rms_norm_modulate(td(x), td(np.ones(cols, np.float32)), td(scale), td(shift),
                                 torch.tensor(idx[:3], device=dev), 1e-6)
+    with pytest.raises(ValueError, match="on the GPU"):  # host indices never reach a kernel
+        fused_modulate(td(x), td(shift), td(scale), torch.tensor(idx))
     with pytest.raises(ValueError, match="multiple of 8"):
         fused_modulate(td(x[:, :12]), td(shift[:, :12]), td(scale[:, :12]), torch.tensor(idx, device=dev))
     torch.cuda.synchronize()
