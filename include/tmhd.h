@@ -59,13 +59,13 @@ typedef struct tmhd_attn_args {
   const void *q;          /* bf16 token-major queries */
   int64_t q_token_stride; /* elements */
   int64_t q_head_stride;  /* elements */
-  const int32_t *q_rows;  /* device row list of length lq, or NULL */
+  const int32_t *q_rows;  /* device row list of length lq, or NULL (entries must be valid rows) */
   int32_t q_row0;         /* first row when q_rows is NULL */
   int32_t lq;             /* query rows */
   void *o;                /* bf16 token-major output */
   int64_t o_token_stride;
   int64_t o_head_stride;
-  const int32_t *o_rows;  /* device row list of length lq, or NULL */
+  const int32_t *o_rows;  /* device row list of length lq, or NULL (entries must be valid rows) */
   int32_t o_row0;
   int32_t heads;
   int32_t head_dim;       /* 64 or 128 */
@@ -150,7 +150,8 @@ int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_quant *quant,
 
 /*
  * Copy `n` token-major K/V rows into a slot at token offset `dst`, then zero
- * slot rows [dst + n, zero_to).  Source row i is rows[i] (or row0 + i).
+ * slot rows [dst + n, zero_to).  Source row i is rows[i] (a device list whose
+ * entries must be valid source rows; the kernel reads through them) or row0 + i.
  * Replaces the index_select staging and torch.cat commit of
  * src/taomate_hd/streaming/cache.py:273-296 and the dense copies of
  * src/taomate_hd/streaming/attention_hook.py:71-91.

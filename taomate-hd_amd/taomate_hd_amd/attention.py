@@ -106,6 +106,20 @@ def _validate_tokens_major(torch: Any, tensor: Any, name: str) -> None:
         raise ValueError(f"{name} must be a [tokens, heads, dim] bf16 view with unit dim stride")
 
 
+def _row_list(torch: Any, rows: Any, device: Any, limit: int, name: str, checked: bool) -> Any:
+    """A row list as a contiguous int32 tensor on ``device`` with entries in
+    [0, limit).  The range check reads the list's min / max back (one sync);
+    callers whose lists are valid by construction pass ``checked``."""
+    if not torch.is_tensor(rows) or rows.device != torch.device(device):
+        raise ValueError(f"{name} must be a tensor on the GPU of the rows it indexes")
+    rows = rows.reshape(-1).to(torch.int32).contiguous()
+    if not checked and rows.numel():
+        lo, hi = (int(v) for v in torch.aminmax(rows))
+        if lo < 0 or hi >= limit:
+            raise ValueError(f"{name} entries must lie in [0, {limit})")
+    return rows
+
+
 def segment_attention(
     torch: Any,
     query: Any,
@@ -123,6 +137,7 @@ def segment_attention(
     split: bool = True,
     return_quant: bool = False,
     timer: ComponentTimer | None = None,
+    rows_checked: bool = False,
 ) -> Any:
     """Attention of the selected query rows over ``segments`` (in place, no mask).
 
@@ -131,6 +146,8 @@ def segment_attention(
     ``out`` a new ``[lq, H, D]`` tensor is returned.  ``split`` lets the
     library run the items of a partial last round as key ranges (merged on
     the same stream); results agree with the unsplit run to fp32 rounding.
+    Row lists are device tensors; their range is checked (one sync) unless
+    ``rows_checked`` says the caller built them in range.
     """
     if backend not in BACKENDS:
         raise ValueError(f"unknown attention backend {backend!r}")
@@ -138,7 +155,7 @@ def segment_attention(
     heads, head_dim = int(query.shape[1]), int(query.shape[2])
     keep: list[Any] = []
     if q_rows is not None:
-        q_rows = q_rows.to(torch.int32).contiguous()
+        q_rows = _row_list(torch, q_rows, query.device, int(query.shape[0]), "q_rows", rows_checked)
         keep.append(q_rows)
         n = int(q_rows.numel())
         if lq is not None and int(lq) != n:
@@ -154,7 +171,7 @@ def segment_attention(
     if tuple(out.shape[1:]) != (heads, head_dim):
         raise ValueError("out heads/dim differ from query")
     if o_rows is not None:
-        o_rows = o_rows.to(torch.int32).contiguous()
+        o_rows = _row_list(torch, o_rows, out.device, int(out.shape[0]), "o_rows", rows_checked)
         keep.append(o_rows)
         if int(o_rows.numel()) != lq:
             raise ValueError("output row list length differs from the query rows")

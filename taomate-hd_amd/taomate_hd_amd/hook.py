@@ -72,7 +72,8 @@ def _live_documents_from_mask_or_hint(
 
 
 class _Rows:
-    """A set of packed-sequence rows: a contiguous range or a device row list."""
+    """A set of packed-sequence rows: a contiguous range or a device row list
+    (built from in-range host rows, so its kernels skip the range check)."""
 
     def __init__(self, torch: Any, absolute: list[int], device: Any) -> None:
         self.count = len(absolute)
@@ -84,17 +85,17 @@ class _Rows:
 
     def query_kwargs(self) -> dict[str, Any]:
         if self.index is not None:
-            return {"q_rows": self.index}
+            return {"q_rows": self.index, "rows_checked": True}
         return {"q_row0": self.start, "lq": self.count}
 
     def out_kwargs(self) -> dict[str, Any]:
         if self.index is not None:
-            return {"o_rows": self.index}
+            return {"o_rows": self.index}  # covered by query_kwargs' rows_checked
         return {"o_row0": self.start}
 
     def pack_kwargs(self) -> dict[str, Any]:
         if self.index is not None:
-            return {"rows": self.index}
+            return {"rows": self.index, "rows_checked": True}
         return {"row0": self.start, "count": self.count}
 
     def host_rows(self) -> list[int]:

@@ -383,7 +383,7 @@ class HeadMajorRingKVCache:
         rows = self._staged_commit_indices
         slot = self._slot_pool(key.device).acquire(int(rows.numel()))
         try:
-            slot.pack(key, value, rows=rows)
+            slot.pack(key, value, rows=rows, rows_checked=True)  # index_select above bounds-checked them
         except BaseException:
             self._pool.release(slot)
             raise

@@ -84,13 +84,14 @@ class KVSlot:
         return SlotView(self, count)
 
     def pack(self, key: Any, value: Any, *, rows: Any | None = None, row0: int = 0, count: int | None = None,
-             dst: int = 0) -> None:
+             dst: int = 0, rows_checked: bool = False) -> None:
         """Copy token-major rows of ``key``/``value`` ([T, H, D] bf16) into the slot.
 
         ``rows`` is an int32/int64 GPU index tensor; without it rows
         ``row0 .. row0 + count`` are copied.  They land at slot rows
         ``dst ..`` (``dst`` a multiple of 64) and the slot rows after them up to
         the next multiple of 64 are zeroed; ``tokens`` becomes the end row.
+        The range of ``rows`` is checked (one sync) unless ``rows_checked``.
         """
         torch = self._torch
         for name, t in (("key", key), ("value", value)):
@@ -103,9 +104,9 @@ class KVSlot:
             raise ValueError(f"K/V heads x dim {tuple(key.shape[1:])} differ from slot {(self.heads, self.head_dim)}")
         rows_ptr = None
         if rows is not None:
-            if rows.dtype != torch.int32:
-                rows = rows.to(torch.int32)
-            rows = rows.contiguous()
+            from .attention import _row_list
+
+            rows = _row_list(torch, rows, key.device, int(key.shape[0]), "rows", rows_checked)
             n = int(rows.numel())
             rows_ptr = _native.ptr(rows) if n else None
         else:

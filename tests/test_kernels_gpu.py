@@ -340,3 +340,34 @@ def test_full_size_stage_shapes_on_sampled_rows(torch_mod, dev, backend, lq, spl
         assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
     else:
         assert oatt.cosine(got, want) >= I8_COSINE
+
+
+def test_row_lists_checked_before_any_launch(torch_mod, dev):
+    """Row lists are device tensors with in-range entries; anything else is
+    refused before a kernel could read through it."""
+    torch = torch_mod
+    from taomate_hd_amd import KVSlot, segment_attention
+
+    H, D, T = 2, 128, 40
+    k = randn_bf16((T, H, D), 1)
+    kd = to_dev(k, dev)
+    q = to_dev(randn_bf16((T, H, D), 2), dev)
+    slot = KVSlot(torch, heads=H, head_dim=D, capacity=64, device=dev)
+    with pytest.raises(ValueError, match="on the GPU"):
+        slot.pack(kd, kd, rows=torch.tensor([0, 1, 2], dtype=torch.int32))
+    with pytest.raises(ValueError, match=r"in \[0, 40\)"):
+        slot.pack(kd, kd, rows=torch.tensor([0, 40], dtype=torch.int32, device=dev))
+    slot.pack(kd, kd, rows=torch.tensor([3, 39, 0], dtype=torch.int32, device=dev))
+    view = [slot.view()]
+    with pytest.raises(ValueError, match="on the GPU"):
+        segment_attention(torch, q, view, scale=0.1, q_rows=torch.tensor([1, 2], dtype=torch.int32))
+    with pytest.raises(ValueError, match=r"in \[0, 40\)"):
+        segment_attention(torch, q, view, scale=0.1, q_rows=torch.tensor([-1, 2], dtype=torch.int32, device=dev))
+    out = torch.zeros((5, H, D), dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError, match=r"in \[0, 5\)"):
+        segment_attention(torch, q, view, scale=0.1, q_rows=torch.tensor([1, 2], dtype=torch.int32, device=dev),
+                          out=out, o_rows=torch.tensor([4, 5], dtype=torch.int32, device=dev))
+    res = segment_attention(torch, q, view, scale=0.1, q_rows=torch.tensor([7, 2], dtype=torch.int32, device=dev),
+                            out=out, o_rows=torch.tensor([4, 0], dtype=torch.int32, device=dev))
+    torch.cuda.synchronize()
+    assert res is out and bool(torch.isfinite(out).all())
