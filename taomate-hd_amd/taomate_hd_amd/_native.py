@@ -203,6 +203,16 @@ def require_device_tensor(torch: Any, tensor: Any, name: str) -> None:
         raise ValueError(f"{name} must be a GPU tensor (the HIP kernels have no CPU path)")
 
 
+def require_same_gpu(torch: Any, device: Any, **tensors: Any) -> None:
+    """Every given tensor (None skipped) lives on ``device``, a GPU."""
+    for name, tensor in tensors.items():
+        if tensor is None:
+            continue
+        require_device_tensor(torch, tensor, name)
+        if tensor.device != device:
+            raise ValueError(f"{name} must be on {device} (found {tensor.device})")
+
+
 def stream_ptr(torch: Any, device: Any) -> int:
     return int(torch.cuda.current_stream(device=device).cuda_stream)
 

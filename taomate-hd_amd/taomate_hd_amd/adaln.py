@@ -30,8 +30,8 @@ def _rows(torch: Any, value: Any, name: str) -> Any:
     return flat
 
 
-def _table(torch: Any, table: Any, name: str, cols: int) -> Any:
-    _native.require_device_tensor(torch, table, name)
+def _table(torch: Any, table: Any, name: str, cols: int, device: Any) -> Any:
+    _native.require_same_gpu(torch, device, **{name: table})
     if table.dtype != torch.bfloat16 or table.ndim != 2 or int(table.shape[-1]) != cols:
         raise ValueError(f"SOL {name} table must be bf16 [table_rows, {cols}]")
     if table.stride(-1) != 1 or table.stride(0) % 8 or table.data_ptr() % 16:
@@ -39,8 +39,8 @@ def _table(torch: Any, table: Any, name: str, cols: int) -> Any:
     return table
 
 
-def _weight(torch: Any, weight: Any, cols: int) -> Any:
-    _native.require_device_tensor(torch, weight, "weight")
+def _weight(torch: Any, weight: Any, cols: int, device: Any) -> Any:
+    _native.require_same_gpu(torch, device, weight=weight)
     if weight.dtype != torch.bfloat16 or int(weight.numel()) != cols:
         raise ValueError("SOL RMSNorm weight must be bf16 with one value per column")
     return weight.reshape(-1).contiguous()
@@ -68,7 +68,7 @@ def fused_rms_norm(value: Any, weight: Any, eps: float) -> Any:
     shape = value.shape
     flat = _rows(torch, value, "value")
     rows, cols = int(flat.shape[0]), int(flat.shape[1])
-    w = _weight(torch, weight, cols)
+    w = _weight(torch, weight, cols, flat.device)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device)
     _run(_native.load().tmhd_rms_norm(_native.ptr(flat), flat.stride(0), _native.ptr(out), out.stride(0),
                                       _native.ptr(w), rows, cols, float(eps), _native.stream_ptr(torch, flat.device)),
@@ -84,8 +84,8 @@ def fused_rms_norm_modulate(value: Any, weight: Any, scale: Any, shift: Any, ind
     flat = _rows(torch, value, "value")
     rows, cols = int(flat.shape[0]), int(flat.shape[1])
     index = _index(torch, indices, rows, "SOL RMSNorm/AdaLN indices do not cover every row", flat.device)
-    w = _weight(torch, weight, cols)
-    scale, shift = _table(torch, scale, "scale", cols), _table(torch, shift, "shift", cols)
+    w = _weight(torch, weight, cols, flat.device)
+    scale, shift = _table(torch, scale, "scale", cols, flat.device), _table(torch, shift, "shift", cols, flat.device)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device)
     _run(_native.load().tmhd_rms_norm_modulate(
         _native.ptr(flat), flat.stride(0), _native.ptr(out), out.stride(0), _native.ptr(w), _native.ptr(scale),
@@ -104,11 +104,12 @@ def fused_residual_gate_rms_norm_modulate(residual: Any, branch: Any, gate: Any,
     res = _rows(torch, residual, "residual")
     rows, cols = int(res.shape[0]), int(res.shape[1])
     br = _rows(torch, branch.reshape(-1, cols), "branch")
+    _native.require_same_gpu(torch, res.device, branch=br)
     if int(br.shape[0]) != rows:
         raise ValueError("SOL residual and branch rows differ")
     index = _index(torch, indices, rows, "SOL residual/AdaLN indices do not cover every row", res.device)
-    w = _weight(torch, weight, cols)
-    gate, scale, shift = (_table(torch, t, n, cols) for t, n in ((gate, "gate"), (scale, "scale"), (shift, "shift")))
+    w = _weight(torch, weight, cols, res.device)
+    gate, scale, shift = (_table(torch, t, n, cols, res.device) for t, n in ((gate, "gate"), (scale, "scale"), (shift, "shift")))
     hidden = torch.empty((rows, cols), dtype=torch.bfloat16, device=res.device)
     out = torch.empty_like(hidden)
     _run(_native.load().tmhd_residual_gate_rms_norm_modulate(
@@ -127,7 +128,7 @@ def fused_modulate(value: Any, shift: Any, scale: Any, indices: Any) -> Any:
     flat = _rows(torch, value, "value")
     rows, cols = int(flat.shape[0]), int(flat.shape[1])
     index = _index(torch, indices, rows, None, flat.device)
-    scale, shift = _table(torch, scale, "scale", cols), _table(torch, shift, "shift", cols)
+    scale, shift = _table(torch, scale, "scale", cols, flat.device), _table(torch, shift, "shift", cols, flat.device)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=flat.device)
     _run(_native.load().tmhd_modulate(
         _native.ptr(flat), flat.stride(0), _native.ptr(out), out.stride(0), _native.ptr(scale), scale.stride(0),
@@ -144,10 +145,11 @@ def fused_gate_add(residual: Any, gate: Any, branch: Any, indices: Any) -> Any:
     res = _rows(torch, residual, "residual")
     rows, cols = int(res.shape[0]), int(res.shape[1])
     br = _rows(torch, branch.reshape(-1, cols), "branch")
+    _native.require_same_gpu(torch, res.device, branch=br)
     if int(br.shape[0]) != rows:
         raise ValueError("SOL residual and branch rows differ")
     index = _index(torch, indices, rows, None, res.device)
-    gate = _table(torch, gate, "gate", cols)
+    gate = _table(torch, gate, "gate", cols, res.device)
     out = torch.empty((rows, cols), dtype=torch.bfloat16, device=res.device)
     _run(_native.load().tmhd_gate_add(
         _native.ptr(res), res.stride(0), _native.ptr(gate), gate.stride(0), _native.ptr(br), br.stride(0),

@@ -58,8 +58,8 @@ def packed_sdpa(q: Any, k: Any, v: Any, *, cu_seqlens: Any, cu_seqlens_host: tup
         raise ValueError("packed attention has no live segment")
     if q.ndim != 3 or k.shape != q.shape or v.shape != q.shape:
         raise ValueError("packed attention Q/K/V must share one [tokens, heads, head_dim] shape")
+    _native.require_same_gpu(torch, q.device, q=q, k=k, v=v)
     for name, t in (("q", q), ("k", k), ("v", v)):
-        _native.require_device_tensor(torch, t, name)
         if t.dtype != torch.bfloat16:
             raise ValueError(f"packed attention {name} must be bfloat16")
     heads, head_dim = int(q.shape[1]), int(q.shape[2])

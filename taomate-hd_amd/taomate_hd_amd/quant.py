@@ -42,6 +42,7 @@ def dynamic_scaled_int8_quant(out: Any, x: Any, scale: Any, azp: Any | None = No
     if azp is not None:
         raise NotImplementedError("asymmetric (azp) INT8 quantization is not implemented")
     _check_rows(torch, x, "x")
+    _native.require_same_gpu(torch, x.device, out=out, scale=scale)
     if x.dtype != torch.bfloat16:
         raise ValueError("x must be bf16")
     rows, cols = int(x.shape[0]), int(x.shape[1])
@@ -129,6 +130,7 @@ def cutlass_scaled_mm_out(out: Any, a: Any, b: Any, scale_a: Any, scale_b: Any, 
     """out = bf16(float(a @ b) * scale_b[n] * scale_a[m] (+ bias[n])), int32 accumulate."""
     torch = _torch()
     m, n, k, lda, ldb = _gemm_operands(torch, a, b)
+    _native.require_same_gpu(torch, a.device, b=b, out=out, scale_a=scale_a, scale_b=scale_b, bias=bias)
     if out.dtype != torch.bfloat16:
         raise NotImplementedError("only bf16 output is implemented")
     if tuple(out.shape) != (m, n) or out.stride(1) != 1:
@@ -167,6 +169,7 @@ def int8_mm_i32(a: Any, b: Any) -> Any:
     """Raw int32 accumulators of ``a @ b`` (same GEMM kernel, no epilogue)."""
     torch = _torch()
     m, n, k, lda, ldb = _gemm_operands(torch, a, b)
+    _native.require_same_gpu(torch, a.device, b=b)
     out = torch.empty((m, n), dtype=torch.int32, device=a.device)
     ws, ws_bytes = _split_workspace(torch, a.device, m, n, k)
     status = _native.load().tmhd_gemm_i8_i32_ws(
