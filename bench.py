@@ -52,6 +52,7 @@ LKV = LQ + ANCHOR + 2 * LQ  # 40,788
 ATTN_FLOPS = 4.0 * H * LQ * LKV * D
 LAYER = "blocks.0.attn"
 M_X, K_X, N_W = 12252, 5120, 13824
+FFN = 14336  # MLP width of the DiT (model/architecture.py:21)
 TRAFFIC_PROFILE = REPO / "profiles" / "attn_fwd_bf16_768p_pmc.txt"
 
 
@@ -204,6 +205,29 @@ def bench_w8a8(torch, dev, steps, warmup):
     return wall_ms, dev_ms, comps
 
 
+def bench_mlp(torch, dev, steps, warmup):
+    """W8A8 FC1 of the DiT MLP on the 768p chunk's hidden rows (LQ x 5376 ->
+    2 x 14336 gate / up columns), followed by SwiGLU: the two-step form
+    (projection written, then fused_swiglu) against the GEMM with the SwiGLU
+    epilogue.  Synthetic bf16 inputs, weights quantized before timing.
+    Returns {name: device ms per call}."""
+    from taomate_hd_amd import (W8A8Workspace, cutlass_w8a8_linear, cutlass_w8a8_linear_swiglu, fused_swiglu,
+                                quantize_cutlass_w8a8_swiglu_weight, quantize_cutlass_w8a8_weight)
+
+    gen = torch.Generator(device=dev).manual_seed(11)
+    x = _randn(torch, (LQ, HIDDEN), gen, dev).to(torch.bfloat16)
+    w = _randn(torch, (2 * FFN, HIDDEN), gen, dev, 0.02).to(torch.bfloat16)
+    qw, sw = quantize_cutlass_w8a8_weight(torch, w)
+    qw_t, sw_t = qw.t(), sw.t()
+    qwi, swi = quantize_cutlass_w8a8_swiglu_weight(torch, w)
+    del w
+    ws = W8A8Workspace(torch)
+    _, two_ms = time_steps(torch, lambda: fused_swiglu(cutlass_w8a8_linear(
+        torch, x, qw, sw, bias=None, workspace=ws, weight_t=qw_t, weight_scale_t=sw_t)), steps, warmup)
+    _, fused_ms = time_steps(torch, lambda: cutlass_w8a8_linear_swiglu(torch, x, qwi, swi, workspace=ws), steps, warmup)
+    return {"two_step": two_ms, "fused": fused_ms}
+
+
 def bench_rope(torch, dev, steps, warmup):
     """Q/K RMSNorm + RoPE in place in the merged QKV projection of the 768p chunk
     (the step in front of the hook), synthetic bf16 inputs; returns ms per call."""
@@ -312,7 +336,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "copy"), default="all")
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "copy"),
+                    default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -487,6 +512,20 @@ def main() -> int:
         if result["value"] is None:
             result["value"], result["ms_per_step"] = result["packed_sdpa"]["tflops"], round(packed_ms, 4)
             result["unit"] = "TFLOPS"
+    if args.workload in ("all", "mlp"):
+        mlp = bench_mlp(torch, dev, args.steps, args.warmup)
+        ops = 2.0 * LQ * HIDDEN * 2 * FFN
+        result["mlp_fc1_swiglu"] = {
+            "two_step_us": round(mlp["two_step"] * 1e3, 1),
+            "fused_us": round(mlp["fused"] * 1e3, 1),
+            "speedup": round(mlp["two_step"] / mlp["fused"], 3),
+            "fused_tops": round(ops / (mlp["fused"] * 1e-3) / 1e12, 1),
+            "shape": f"rows {LQ}, hidden {HIDDEN}, 2 x {FFN} gate / up columns, token quant included",
+        }
+        _log(f"mlp fc1+swiglu: two-step {mlp['two_step']:.3f} ms, fused {mlp['fused']:.3f} ms")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["mlp_fc1_swiglu"]["fused_tops"], round(mlp["fused"], 4)
+            result["unit"] = "TOPS"
     if not args.no_cpu_baseline and args.workload in ("all", "bf16"):
         result["cpu_baseline"] = cpu_baseline(torch)
         _log(f"cpu baseline: {result['cpu_baseline']}")

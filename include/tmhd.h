@@ -359,6 +359,25 @@ int tmhd_gemm_i8_i32_ws(int32_t *out, const int8_t *a, const int8_t *b, int32_t 
                         int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *workspace,
                         int64_t workspace_bytes, void *stream);
 
+/*
+ * No counterpart in the reference as one call: FC1 of the DiT MLP followed by
+ * SwiGLU (fused_kernels.py:694-704 applied to the W8A8 projection,
+ * model/layers.py:525-534), without writing the [m][n] projection.  b holds
+ * the n = 2 * f weight rows interleaved in blocks of 256: rows [256t,
+ * 256t + 128) are gate rows [128t, 128t + 128) and rows [256t + 128,
+ * 256t + 256) the matching up rows; b_scale (and bias) follow the same
+ * order.  out[m][j] (j < n / 2, row stride ldo) = R(R(g * sigmoid(g)) * u)
+ * of g, u = the bf16 projection values of tmhd_gemm_w8a8 for gate j and up j,
+ * the SwiGLU of tmhd_swiglu: bit-identical to tmhd_gemm_w8a8 then
+ * tmhd_swiglu on the de-interleaved projection.  n a multiple of 256, k of
+ * 64; out 16-byte aligned rows; same optional split workspace as
+ * tmhd_gemm_w8a8_ws.
+ */
+int tmhd_gemm_w8a8_swiglu_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
+                             const float *b_scale, const void *bias, int32_t m, int32_t n,
+                             int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *workspace,
+                             int64_t workspace_bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

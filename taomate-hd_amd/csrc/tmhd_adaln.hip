@@ -184,12 +184,7 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const uint16_t *x, int64_t 
     const i32x4 u = *(const i32x4 *)(x + r * x_stride + half + c);
     i32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float g0 = lo_f32((uint32_t)g[e]), g1 = hi_f32((uint32_t)g[e]);
-      const float s0 = __fdiv_rn(1.0f, 1.0f + expf(-g0)), s1 = __fdiv_rn(1.0f, 1.0f + expf(-g1));
-      const uint32_t act = pack_bf16_rne(g0 * s0, g1 * s1);
-      o[e] = (int)pack_bf16_rne(lo_f32(act) * lo_f32((uint32_t)u[e]), hi_f32(act) * hi_f32((uint32_t)u[e]));
-    }
+    for (int e = 0; e < 4; ++e) o[e] = (int)swiglu_pair((uint32_t)g[e], (uint32_t)u[e]);
     *(i32x4 *)(out + r * out_stride + c) = o;
   }
 }

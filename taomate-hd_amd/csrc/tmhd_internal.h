@@ -49,6 +49,19 @@ __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 
+// SwiGLU of one packed bf16 pair of gates and ups: R(R(g * sigmoid(g)) * u),
+// sigmoid(g) = 1 / (1 + exp(-g)) with the accurate single-precision exp and a
+// correctly rounded division (shared by the SwiGLU kernel and the GEMM's
+// fused SwiGLU epilogue, so both give the same bits).
+__device__ __forceinline__ uint32_t swiglu_pair(uint32_t g, uint32_t u) {
+#pragma clang fp contract(off)
+  const float g0 = __uint_as_float(g << 16), g1 = __uint_as_float(g & 0xffff0000u);
+  const float s0 = __fdiv_rn(1.0f, 1.0f + expf(-g0)), s1 = __fdiv_rn(1.0f, 1.0f + expf(-g1));
+  const uint32_t act = pack_bf16_rne(g0 * s0, g1 * s1);
+  return pack_bf16_rne(__uint_as_float(act << 16) * __uint_as_float(u << 16),
+                       __uint_as_float(act & 0xffff0000u) * __uint_as_float(u & 0xffff0000u));
+}
+
 // Correctly rounded square root of x >= 0 (+inf and NaN pass through).  The
 // hardware square root is within one ulp; the Tuckerman rounding test picks
 // between it and its two neighbours s- < s < s+: sqrt(x) lies below the

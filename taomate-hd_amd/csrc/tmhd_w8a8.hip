@@ -362,7 +362,11 @@ __device__ __forceinline__ void hload_lds16(const void *base, uint32_t off, uint
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
-template <bool RAW, bool SPLIT>
+// GLU: the weight rows come in blocks of 256 (128 gate rows, then the 128
+// matching up rows), so tile column c < 128 and c + 128 are the gate and up of
+// one output column; the epilogue writes SwiGLU(gate, up) of the bf16
+// projection, out[m][n0 / 2 + c] (ldo counts its columns).
+template <bool RAW, bool SPLIT, bool GLU = false>
 __global__ void __launch_bounds__(HWAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma clang fp contract(off)
@@ -562,6 +566,24 @@ gemm_i8_wave128_kernel(const GArgs ga) {
                       (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
           }
       }
+      if constexpr (GLU) {
+        // gate halves sit in the staging rows of waves (wm, 0), up halves in
+        // (wm, 1); each wave writes 64 of the tile's 256 output rows
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+          const int r = w * 64 + it * 4 + (lane >> 4), c = lane & 15;
+          const int wr = r >> 7, rr = r & 127;
+          const i32x4 gv = *(const i32x4 *)(smem + (uint32_t)((wr * 2) * 128 * ROWB + rr * ROWB + c * 16));
+          const i32x4 uv = *(const i32x4 *)(smem + (uint32_t)((wr * 2 + 1) * 128 * ROWB + rr * ROWB + c * 16));
+          i32x4 o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[e] = (int)swiglu_pair((uint32_t)gv[e], (uint32_t)uv[e]);
+          const int m = m0 + r, n = n0 / 2 + c * 8;
+          if (m < ga.m) *(i32x4 *)((uint16_t *)ga.out + (int64_t)m * ga.ldo + n) = o;
+        }
+        return;
+      }
 #pragma unroll
       for (int it = 0; it < 32; ++it) {
         const int r = it * 4 + (lane >> 4), c = lane & 15;
@@ -579,6 +601,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       return;
     }
   }
+  if constexpr (GLU) return;  // the GLU launcher always takes the staged path above
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int m = m0 + wm * 128 + j * 32 + lr;
@@ -623,6 +646,40 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       }
     }
   }
+}
+
+// Merge of the K-split GLU tiles: gate columns c .. c + 3 and up columns
+// 128 + c .. of one row, each the sum of its partials, dequantised and
+// rounded as the GEMM's epilogue does, then SwiGLU.  Block: 8 rows of one
+// tile, 4 output columns per thread.
+__global__ void __launch_bounds__(256) gemm_split_merge_glu_kernel(const GArgs ga) {
+  const int item = blockIdx.x / (HBM_ / 8);
+  const int r = (blockIdx.x % (HBM_ / 8)) * 8 + (threadIdx.x >> 5);
+  const int c = (threadIdx.x & 31) * 4;
+  int tm, tn;
+  grouped_tile(ga.full + item, ga.tm_count, ga.tn_count, tm, tn);
+  const int m = tm * HBM_ + r, n0 = tn * HBN;
+  if (m >= ga.m) return;
+  const int32_t *wp = ga.ws + (int64_t)item * ga.nsplit * (HBM_ * HBN) + r * HBN + c;
+  i32x4 ag = *(const i32x4 *)wp, au = *(const i32x4 *)(wp + 128);
+  for (int p = 1; p < ga.nsplit; ++p) {
+    ag += *(const i32x4 *)(wp + (int64_t)p * (HBM_ * HBN));
+    au += *(const i32x4 *)(wp + (int64_t)p * (HBM_ * HBN) + 128);
+  }
+  const float asm_ = ga.as[m];
+  float tg[4], tu[4];
+  uint16_t vg[4], vu[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int ng = n0 + c + e, nu = ng + 128;
+    tg[e] = dequant_f32(ag[e], ga.bs[ng], asm_, ga.bias != nullptr, ga.bias ? ga.bias[ng] : 0u);
+    tu[e] = dequant_f32(au[e], ga.bs[nu], asm_, ga.bias != nullptr, ga.bias ? ga.bias[nu] : 0u);
+  }
+  bf16_quad(tg, vg);
+  bf16_quad(tu, vu);
+  const uint32_t o0 = swiglu_pair((uint32_t)vg[0] | ((uint32_t)vg[1] << 16), (uint32_t)vu[0] | ((uint32_t)vu[1] << 16));
+  const uint32_t o1 = swiglu_pair((uint32_t)vg[2] | ((uint32_t)vg[3] << 16), (uint32_t)vu[2] | ((uint32_t)vu[3] << 16));
+  *(i32x2 *)((uint16_t *)ga.out + (int64_t)m * ga.ldo + n0 / 2 + c) = i32x2{(int)o0, (int)o1};
 }
 
 // Merge of the K-split tiles: the sum of each tile's nsplit int32 partials
@@ -724,6 +781,46 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
   return check_launch(what);
 }
 
+// The GEMM with the SwiGLU epilogue: out[m][n / 2] from gate / up rows
+// interleaved in blocks of 128 (see the GLU kernel).  Only the one-wave-per-
+// SIMD kernel and its k-split carry the GLU epilogue.
+int launch_gemm_glu(void *out, const int8_t *a, const int8_t *b, const float *as, const float *bs, const void *bias,
+                    int32_t m, int32_t n, int32_t k, int64_t lda, int64_t ldb, int64_t ldo, void *ws,
+                    int64_t ws_bytes, void *stream) {
+  const char *what = "tmhd_gemm_w8a8_swiglu_ws";
+  if (m < 0 || n <= 0 || k <= 0) return set_error(TMHD_ERR_INVALID, "%s: m %d n %d k %d", what, m, n, k);
+  if (k % HKS || n % 256)
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: k %d (a multiple of %d), n %d (gate + up, a multiple of 256)", what,
+                     k, HKS, n);
+  if (!out || !a || !b || !as || !bs) return set_error(TMHD_ERR_INVALID, "%s: null pointer", what);
+  if (((uintptr_t)a % 16) || ((uintptr_t)b % 16) || lda % 16 || ldb % 16 || lda < k || ldb < k || ldo < n / 2 ||
+      ((uintptr_t)out % 16) || ldo % 8)
+    return set_error(TMHD_ERR_INVALID, "%s: operands and output must be 16-byte aligned rows", what);
+  if (m == 0) return TMHD_OK;
+  if (!((int64_t)(m - 1) * lda + k < ((int64_t)1 << 32) && (int64_t)(n - 1) * ldb + k < ((int64_t)1 << 32)))
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: operands beyond 32-bit row offsets", what);
+  const int64_t tiles = (int64_t)((m + HBM_ - 1) / HBM_) * (n / HBN);
+  GArgs ga{a, b, out, as, bs, (const uint16_t *)bias, m, n, k, lda, ldb, ldo, (m + HBM_ - 1) / HBM_, n / HBN,
+           (int32_t)(((uintptr_t)bs % 16) == 0 && ((uintptr_t)bias % 8) == 0), 1, (int32_t)tiles, 1, nullptr};
+  int tail = 0, parts = 1;
+  gemm_split_plan(m, n, k, tail, parts);
+  if (parts > 1 && ws && ((uintptr_t)ws % 16) == 0 && ws_bytes >= gemm_split_bytes(tail, parts)) {
+    ga.full = (int32_t)(tiles - tail);
+    ga.nsplit = parts;
+    ga.ws = (int32_t *)ws;
+  }
+  hipStream_t s = (hipStream_t)stream;
+  if (ga.full > 0)
+    hipLaunchKernelGGL((gemm_i8_wave128_kernel<false, false, true>), dim3((unsigned)ga.full), dim3(HWAVES * 64), 0, s,
+                       ga);
+  if (ga.nsplit > 1) {
+    hipLaunchKernelGGL((gemm_i8_wave128_kernel<false, true>), dim3((unsigned)(tail * parts)), dim3(HWAVES * 64), 0, s,
+                       ga);
+    hipLaunchKernelGGL(gemm_split_merge_glu_kernel, dim3((unsigned)(tail * (HBM_ / 8))), dim3(256), 0, s, ga);
+  }
+  return check_launch(what);
+}
+
 }  // namespace
 }  // namespace tmhd
 
@@ -765,4 +862,12 @@ extern "C" int tmhd_gemm_i8_i32_ws(int32_t *out, const int8_t *a, const int8_t *
                                    void *stream) {
   return tmhd::launch_gemm<true>(out, a, b, nullptr, nullptr, nullptr, m, n, k, lda, ldb, ldo, workspace,
                                  workspace_bytes, stream);
+}
+
+extern "C" int tmhd_gemm_w8a8_swiglu_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,
+                                        const float *b_scale, const void *bias, int32_t m, int32_t n, int32_t k,
+                                        int64_t lda, int64_t ldb, int64_t ldo, void *workspace,
+                                        int64_t workspace_bytes, void *stream) {
+  return tmhd::launch_gemm_glu(out, a, b, a_scale, b_scale, bias, m, n, k, lda, ldb, ldo, workspace, workspace_bytes,
+                               stream);
 }

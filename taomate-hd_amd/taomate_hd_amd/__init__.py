@@ -56,7 +56,10 @@ from .w8a8 import (
     CutlassW8A8Workspace,
     W8A8Workspace,
     cutlass_w8a8_linear,
+    cutlass_w8a8_linear_swiglu,
+    interleave_swiglu_rows,
     linear,
+    quantize_cutlass_w8a8_swiglu_weight,
     quantize_cutlass_w8a8_weight,
     register_torch_ops,
     resolve_h3_cutlass_w8a8_policy,
@@ -98,12 +101,15 @@ __all__ = [
     "cutlass_scaled_mm",
     "cutlass_scaled_mm_out",
     "cutlass_w8a8_linear",
+    "cutlass_w8a8_linear_swiglu",
+    "interleave_swiglu_rows",
     "dynamic_scaled_int8_quant",
     "int8_mm_i32",
     "kv_contract_from_model",
     "linear",
     "native_stream_attention_hook",
     "native_stream_attention_metadata",
+    "quantize_cutlass_w8a8_swiglu_weight",
     "quantize_cutlass_w8a8_weight",
     "quantize_weight",
     "register_torch_ops",

@@ -150,6 +150,11 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64,
          c_int64, c_void_p, c_int64, c_void_p],
     ),
+    "tmhd_gemm_w8a8_swiglu_ws": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64,
+         c_int64, c_void_p, c_int64, c_void_p],
+    ),
     "tmhd_gemm_i8_i32_ws": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int64, c_int64, c_int64, c_void_p, c_int64,

@@ -178,3 +178,33 @@ def int8_mm_i32(a: Any, b: Any) -> Any:
     )
     _native.check(status, "tmhd_gemm_i8_i32_ws")
     return out
+
+
+def cutlass_scaled_mm_swiglu(a: Any, b: Any, scale_a: Any, scale_b: Any, bias: Any | None = None) -> Any:
+    """SwiGLU of the scaled INT8 GEMM without materialising it: ``b`` is the
+    [K, 2F] column-major view of gate / up weight rows interleaved in blocks
+    of 128 (``interleave_swiglu_rows``), ``scale_b`` (and ``bias``) in the same
+    order; returns ``[M, F]`` bf16 = fused_swiglu(cutlass_scaled_mm(...)) of
+    the de-interleaved weight, bit for bit."""
+    torch = _torch()
+    m, n, k, lda, ldb = _gemm_operands(torch, a, b)
+    _native.require_same_gpu(torch, a.device, b=b, scale_a=scale_a, scale_b=scale_b, bias=bias)
+    sa = scale_a.reshape(-1)
+    sb = scale_b.reshape(-1)
+    if sa.dtype != torch.float32 or sb.dtype != torch.float32 or sa.numel() != m or sb.numel() != n:
+        raise ValueError("scale_a must hold M and scale_b N fp32 values (per-token / per-channel)")
+    sa, sb = sa.contiguous(), sb.contiguous()
+    bias_ptr = None
+    if bias is not None:
+        if bias.dtype != torch.bfloat16 or bias.numel() != n:
+            raise ValueError("bias must be a bf16 vector of N values")
+        bias = bias.contiguous()
+        bias_ptr = _native.ptr(bias)
+    out = torch.empty((m, n // 2), dtype=torch.bfloat16, device=a.device)
+    ws, ws_bytes = _split_workspace(torch, a.device, m, n, k)
+    status = _native.load().tmhd_gemm_w8a8_swiglu_ws(
+        _native.ptr(out), _native.ptr(a), _native.ptr(b), _native.ptr(sa), _native.ptr(sb), bias_ptr,
+        m, n, k, lda, ldb, out.stride(0), ws, ws_bytes, _native.stream_ptr(torch, a.device),
+    )
+    _native.check(status, "tmhd_gemm_w8a8_swiglu_ws")
+    return out

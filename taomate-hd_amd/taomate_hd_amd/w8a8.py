@@ -127,6 +127,43 @@ def cutlass_w8a8_linear(
     return output.reshape(shape)
 
 
+def interleave_swiglu_rows(t: Any) -> Any:
+    """Rows of a fused gate / up tensor ``[2F, ...]`` (gate rows first, as the
+    MLP's merged FC1 stores them, model/layers.py:497-511) reordered in blocks
+    of 128: gate rows 128t.. then up rows 128t.., so that one 256-row GEMM tile
+    holds both halves of 128 output columns.  F must be a multiple of 128."""
+    n = int(t.shape[0])
+    if n % 256:
+        raise ValueError("gate / up rows must be a multiple of 256 (F a multiple of 128)")
+    return t.reshape(2, n // 256, 128, *t.shape[1:]).transpose(0, 1).reshape(t.shape).contiguous()
+
+
+def quantize_cutlass_w8a8_swiglu_weight(torch: Any, weight: Any) -> tuple[Any, Any]:
+    """Per-channel INT8 FC1 weight (gate rows, then up rows) for
+    ``cutlass_w8a8_linear_swiglu``: quantized as ``quantize_cutlass_w8a8_weight``
+    (per row, so the row order does not change the values), then interleaved."""
+    qw, sw = quantize_cutlass_w8a8_weight(torch, weight)
+    return interleave_swiglu_rows(qw), interleave_swiglu_rows(sw)
+
+
+def cutlass_w8a8_linear_swiglu(torch: Any, inputs: Any, weight: Any, weight_scale: Any, *,
+                               bias: Any | None = None, workspace: W8A8Workspace | None = None) -> Any:
+    """``fused_swiglu(cutlass_w8a8_linear(inputs, W1))`` of the MLP
+    (model/layers.py:525-534) in one GEMM whose epilogue applies SwiGLU, so
+    the [M, 2F] projection is never written.  ``weight`` / ``weight_scale``
+    come from ``quantize_cutlass_w8a8_swiglu_weight``; returns ``[..., F]``,
+    bit-identical to the two-step form."""
+    shape = (*inputs.shape[:-1], int(weight.shape[0]) // 2)
+    flattened = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
+    if workspace is not None:
+        quantized, activation_scale = workspace._activation_buffers(flattened, workspace._stream_key(flattened))
+        quant.dynamic_scaled_int8_quant(quantized, flattened, activation_scale, None)
+    else:
+        quantized, activation_scale, _ = quant.scaled_int8_quant(flattened)
+    out = quant.cutlass_scaled_mm_swiglu(quantized, weight.t(), activation_scale, weight_scale.t(), bias)
+    return out.reshape(shape)
+
+
 def linear(
     torch: Any,
     inputs: Any,

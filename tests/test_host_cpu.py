@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
 
     lib = _native.load()
     declared = _declared_symbols()
-    assert len(declared) == 24
+    assert len(declared) == 25
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED_SYMBOLS)
@@ -247,3 +247,20 @@ def test_packed_sdpa_boundary_validation_without_gpu():
         packed_sdpa(q[:0], q[:0], q[:0], cu_seqlens=None, cu_seqlens_host=(0, 0, 0), max_seqlen=0, scale=0.1)
     with pytest.raises(ValueError, match="GPU tensor"):  # valid boundaries: the HIP path is required
         packed_sdpa(q, q, q, cu_seqlens=None, cu_seqlens_host=(0, 4, 10), max_seqlen=6, scale=0.1)
+
+
+def test_swiglu_row_interleave_layout_without_gpu():
+    # gate rows [0, F) then up rows [F, 2F) -> per 256-row tile t: gate 128t.., then up 128t..
+    import torch
+    from taomate_hd_amd import interleave_swiglu_rows
+
+    f = 384
+    rows = torch.arange(2 * f)
+    got = interleave_swiglu_rows(rows.view(2 * f, 1)).view(-1).tolist()
+    want = []
+    for t in range(f // 128):
+        want += list(range(128 * t, 128 * t + 128)) + list(range(f + 128 * t, f + 128 * t + 128))
+    assert got == want
+    assert interleave_swiglu_rows(rows).tolist() == want  # 1-D (bias, scale vectors) too
+    with pytest.raises(ValueError, match="multiple of 256"):
+        interleave_swiglu_rows(torch.arange(2 * 200))

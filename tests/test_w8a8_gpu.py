@@ -6,6 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import bf16
+from oracle import adaln as oada
 from oracle import quant as oq
 from tests.helpers import randn_bf16, to_dev
 
@@ -92,3 +93,33 @@ def test_w8a8_projection_full_size_sampled_rows(torch_mod, dev):
     want = _expected(x, bf16.from_torch(wd), bf16.from_torch(bd))
     got = bf16.from_torch(out[torch.tensor(rows, device=dev)].contiguous())
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,k,f,with_bias", [(300, 1024, 384, False), (130, 256, 128, False), (3 * 256 + 40, 2048, 1024, False),
+                                             (300, 1024, 384, True), (130, 256, 128, True)])
+def test_fused_fc1_swiglu_equals_two_step(torch_mod, dev, m, k, f, with_bias):
+    """FC1 with the SwiGLU epilogue (interleaved gate / up rows) against the
+    two-step path (the W8A8 projection, then fused_swiglu), bit for bit; the
+    first and last shapes run the k-split merge, the middle one does not."""
+    torch = torch_mod
+    from taomate_hd_amd import (W8A8Workspace, cutlass_w8a8_linear, cutlass_w8a8_linear_swiglu, fused_swiglu,
+                                interleave_swiglu_rows, quantize_cutlass_w8a8_swiglu_weight,
+                                quantize_cutlass_w8a8_weight)
+
+    x = to_dev(randn_bf16((m, k), 80 + m), dev)
+    w = to_dev(randn_bf16((2 * f, k), 81 + m, std=0.03), dev)
+    bias = to_dev(randn_bf16((2 * f,), 82 + m, std=0.5), dev) if with_bias else None
+    qw, sw = quantize_cutlass_w8a8_weight(torch, w)
+    two_step = fused_swiglu(cutlass_w8a8_linear(torch, x, qw, sw, bias=bias))
+    qwi, swi = quantize_cutlass_w8a8_swiglu_weight(torch, w)
+    bias_i = None if bias is None else interleave_swiglu_rows(bias)
+    fused = cutlass_w8a8_linear_swiglu(torch, x, qwi, swi, bias=bias_i, workspace=W8A8Workspace(torch) if with_bias else None)
+    torch.cuda.synchronize()
+    assert tuple(fused.shape) == (m, f)
+    assert torch.equal(fused.view(torch.int16), two_step.view(torch.int16))
+    # the oracle's rounding chain for the projection, then SwiGLU within one bf16 ulp
+    proj = _expected(bf16.from_torch(x), bf16.from_torch(w), None if bias is None else bf16.from_torch(bias))
+    want = oada.swiglu(proj)
+    got = bf16.from_torch(fused)
+    ulps = np.abs((got.view(np.int32).astype(np.int64) >> 16) - (want.view(np.int32).astype(np.int64) >> 16))
+    assert ulps.max() <= 1 and np.mean(ulps == 0) >= 0.999
