@@ -189,6 +189,25 @@ int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int32_t head_di
                        void *stream);
 
 /*
+ * tmhd_qkv_norm_rope followed by tmhd_kv_pack of the K and V thirds of tokens
+ * [stage_row0, stage_row0 + stage_n) into a slot at row `dst` (zeroing slot
+ * rows [dst + stage_n, zero_to)), with the same results, in one pass over Q
+ * and K: the normalised, rotated K rows go to the slot as they are written
+ * back, and only V is read again (for its transpose).  qkv rows must be
+ * 16-byte aligned; the slot arguments are those of tmhd_kv_pack.  Replaces
+ * the preprocessing of src/taomate_hd/inference/fused_kernels.py:824-873
+ * together with the chunk's K/V staging copy in front of the hook
+ * (src/taomate_hd/streaming/attention_hook.py:71-91, cache.py:273-296).
+ */
+int tmhd_qkv_norm_rope_stage(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim,
+                             int64_t row_stride, const void *q_weight, const void *k_weight,
+                             const void *cos_sin, int64_t cos_sin_stride, int64_t cos_sin_rows,
+                             int32_t rotary_dim, const int64_t *positions, float eps,
+                             int32_t stage_row0, int32_t stage_n, void *k_slot, void *vt_slot,
+                             int64_t k_head_stride, int64_t vt_head_stride, int32_t vt_row_stride,
+                             int32_t dst, int32_t zero_to, void *stream);
+
+/*
  * The same RMSNorm + RoPE on one projection value[tokens][heads][head_dim]
  * (row stride value_stride elements, heads * head_dim contiguous), written to
  * out (row stride out_stride; out == value with equal strides is in place,

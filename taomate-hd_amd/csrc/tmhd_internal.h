@@ -22,6 +22,13 @@ int set_error(int status, const char *fmt, ...) __attribute__((format(printf, 2,
 int check_launch(const char *what);
 // Compute units of the current device (cached per device; 0 if unknown).
 int device_cus();
+// tmhd_kv_pack with two switches: with_k false leaves the key rows of the
+// data positions to the caller (zero positions are still cleared);
+// check_only validates the arguments and launches nothing.
+int kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_stride, const int32_t *rows,
+            int32_t row0, int32_t n, void *k_slot, void *vt_slot, int64_t k_head_stride, int64_t vt_head_stride,
+            int32_t vt_row_stride, int32_t dst, int32_t zero_to, int32_t heads, int32_t head_dim, void *stream,
+            bool with_k, bool check_only);
 
 // bf16 bits -> fp32 (exact).
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {

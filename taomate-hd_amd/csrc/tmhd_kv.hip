@@ -13,7 +13,9 @@ constexpr int kTile = 64;
 // tmhd_kv_pack: one workgroup = 64 slot positions of one head.
 // Position p of the slot is: data row (p - dst) if dst <= p < dst + n,
 // zero if dst + n <= p < zero_to, untouched otherwise.
-template <int D>
+// WITH_K false: the key rows of data positions are left to the caller (the
+// staged norm + RoPE kernel writes them); zero positions are still cleared.
+template <int D, bool WITH_K = true>
 __global__ void __launch_bounds__(256) kv_pack_kernel(const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
                                                       int64_t ts, int64_t hs, const int32_t *__restrict__ rows,
                                                       int32_t row0, int32_t n, uint16_t *__restrict__ ks,
@@ -37,10 +39,10 @@ __global__ void __launch_bounds__(256) kv_pack_kernel(const uint16_t *__restrict
     if (kind == 1) {
       const int i = p - dst;
       const int64_t src = (int64_t)(rows ? rows[i] : row0 + i) * ts + (int64_t)h * hs + ch * 8;
-      kv = *(const i32x4 *)(k + src);
+      if constexpr (WITH_K) kv = *(const i32x4 *)(k + src);
       vv = *(const i32x4 *)(v + src);
     }
-    if (kind != 0) *(i32x4 *)(ks + (int64_t)h * khs + (int64_t)p * D + ch * 8) = kv;
+    if (WITH_K ? kind != 0 : kind == 2) *(i32x4 *)(ks + (int64_t)h * khs + (int64_t)p * D + ch * 8) = kv;
     const uint32_t *vw = (const uint32_t *)&vv;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -258,11 +260,12 @@ int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s
 }  // namespace
 }  // namespace tmhd
 
-extern "C" int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_stride,
-                            const int32_t *rows, int32_t row0, int32_t n, void *k_slot, void *vt_slot,
-                            int64_t k_head_stride, int64_t vt_head_stride, int32_t vt_row_stride, int32_t dst,
-                            int32_t zero_to, int32_t heads, int32_t head_dim, void *stream) {
-  using namespace tmhd;
+namespace tmhd {
+
+int kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_stride, const int32_t *rows,
+            int32_t row0, int32_t n, void *k_slot, void *vt_slot, int64_t k_head_stride, int64_t vt_head_stride,
+            int32_t vt_row_stride, int32_t dst, int32_t zero_to, int32_t heads, int32_t head_dim, void *stream,
+            bool with_k, bool check_only) {
   if (head_dim != 64 && head_dim != 128) return set_error(TMHD_ERR_UNSUPPORTED, "kv_pack: head_dim %d", head_dim);
   if (n < 0 || dst < 0 || heads <= 0) return set_error(TMHD_ERR_INVALID, "kv_pack: n %d dst %d heads %d", n, dst, heads);
   const int end = max(dst + n, zero_to);
@@ -276,18 +279,33 @@ extern "C" int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride, 
       (n > 0 && (!aligned(k, 16) || !aligned(v, 16))) || token_stride % 8 || head_stride % 8 || k_head_stride % 8 ||
       vt_head_stride % 8)
     return set_error(TMHD_ERR_INVALID, "kv_pack: pointers and strides must be 16-byte aligned");
-  if (p_end == p_begin) return TMHD_OK;
+  if (check_only || p_end == p_begin) return TMHD_OK;
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((p_end - p_begin) / kTile, heads);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(kv_pack_kernel<128>, grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v,
-                       token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,
-                       k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin);
+#define TMHD_PACK(DIM, WK)                                                                                      \
+  hipLaunchKernelGGL((kv_pack_kernel<DIM, WK>), grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v, \
+                     token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,          \
+                     k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin)
+  if (head_dim == 128 && with_k)
+    TMHD_PACK(128, true);
+  else if (head_dim == 128)
+    TMHD_PACK(128, false);
+  else if (with_k)
+    TMHD_PACK(64, true);
   else
-    hipLaunchKernelGGL(kv_pack_kernel<64>, grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v,
-                       token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,
-                       k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin);
+    TMHD_PACK(64, false);
+#undef TMHD_PACK
   return check_launch("tmhd_kv_pack");
+}
+
+}  // namespace tmhd
+
+extern "C" int tmhd_kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_stride,
+                            const int32_t *rows, int32_t row0, int32_t n, void *k_slot, void *vt_slot,
+                            int64_t k_head_stride, int64_t vt_head_stride, int32_t vt_row_stride, int32_t dst,
+                            int32_t zero_to, int32_t heads, int32_t head_dim, void *stream) {
+  return tmhd::kv_pack(k, v, token_stride, head_stride, rows, row0, n, k_slot, vt_slot, k_head_stride, vt_head_stride,
+                       vt_row_stride, dst, zero_to, heads, head_dim, stream, true, false);
 }
 
 extern "C" int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_quant *quant, void *stream) {

@@ -53,6 +53,11 @@ struct RopeArgs {
   int64_t cs_rows;             // TABLE only: positions are clamped to [0, cs_rows)
   int32_t tokens, heads, parts, rotary;  // parts: 2 = Q then K of each token, 1 = one projection
   float eps;
+  // STAGE only: K rows of tokens [stage_row0, stage_row0 + stage_n) are also
+  // written to slot row stage_dst + (t - stage_row0) of kslot (head stride kslot_hs)
+  uint16_t *kslot;
+  int64_t kslot_hs;
+  int32_t stage_row0, stage_n, stage_dst;
 };
 
 constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad in the inverse RMS pass
@@ -60,7 +65,8 @@ constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad i
 // TABLE: cos / sin of channel d at cos_sin[positions[t]][d % h] and [h + d % h]
 // (the merged-projection form); otherwise at cos[t][d] and sin[t][d].
 // NORM false: the rotation alone, applied to the input values (no RMSNorm).
-template <int D, bool TABLE, bool NORM = true>
+// STAGE: the K rows of the staged token range also go to the slot.
+template <int D, bool TABLE, bool NORM = true, bool STAGE = false>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPR = D / 8;     // lanes per row
@@ -74,7 +80,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
   const int oa = rotates ? 4 * j : a.rotary + 8 * (j - rot_lanes);  // channel of piece A
   const int ob = rotates ? half + 4 * j : oa + 4;                   // channel of piece B
   int64_t src_off[U], dst_off[U];
-  int tok[U];
+  int tok[U], part_row[U];
   bool live[U], is_k[U];
   int64_t pos[U];
   int token = row0 / per_token, rem = row0 - token * per_token;
@@ -88,6 +94,7 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
     const int t = live[u] ? token : a.tokens - 1;  // lanes past the end compute a copy of the last row, unstored
     const int r = live[u] ? rem : per_token - 1;
     tok[u] = t;
+    part_row[u] = r;
     is_k[u] = r >= a.heads;
     src_off[u] = (int64_t)t * a.src_stride + (int64_t)r * D;
     dst_off[u] = (int64_t)t * a.dst_stride + (int64_t)r * D;
@@ -192,17 +199,38 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
     if (live[u]) {
       *(i32x2 *)(a.dst + dst_off[u] + oa) = i32x2{(int)out[0], (int)out[1]};
       *(i32x2 *)(a.dst + dst_off[u] + ob) = i32x2{(int)out[2], (int)out[3]};
+      if constexpr (STAGE) {
+        const int i = tok[u] - a.stage_row0;
+        if (is_k[u] && i >= 0 && i < a.stage_n) {
+          uint16_t *row = a.kslot + (int64_t)(part_row[u] - a.heads) * a.kslot_hs + (int64_t)(a.stage_dst + i) * D;
+          *(i32x2 *)(row + oa) = i32x2{(int)out[0], (int)out[1]};
+          *(i32x2 *)(row + ob) = i32x2{(int)out[2], (int)out[3]};
+        }
+      }
     }
   }
 }
 
-int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what, bool norm = true) {
+int rope_rows_check(const RopeArgs &a, int head_dim, const char *what) {
   const int64_t rows = (int64_t)a.tokens * a.parts * a.heads;
   const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
   if (rows > 0x7fffffff - rows_per_block) return set_error(TMHD_ERR_UNSUPPORTED, "%s: too many rows", what);
+  return TMHD_OK;
+}
+
+int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what, bool norm = true,
+                bool stage = false) {
+  if (int st = rope_rows_check(a, head_dim, what)) return st;
+  const int64_t rows = (int64_t)a.tokens * a.parts * a.heads;
+  const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
   const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
   hipStream_t s = (hipStream_t)stream;
-  if (!norm) {
+  if (stage) {
+    if (head_dim == 128)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, true, true, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, true, true, true>), grid, block, 0, s, a);
+  } else if (!norm) {
     if (head_dim == 128)
       hipLaunchKernelGGL((qk_norm_rope_kernel<128, false, false>), grid, block, 0, s, a);
     else
@@ -223,12 +251,13 @@ bool aligned8(const void *p) { return ((uintptr_t)p % 8) == 0; }
 }  // namespace
 }  // namespace tmhd
 
-extern "C" int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim, int64_t row_stride,
-                                  const void *q_weight, const void *k_weight, const void *cos_sin,
-                                  int64_t cos_sin_stride, int64_t cos_sin_rows, int32_t rotary_dim,
-                                  const int64_t *positions, float eps, void *stream) {
-  using namespace tmhd;
-  const char *what = "tmhd_qkv_norm_rope";
+namespace tmhd {
+namespace {
+
+// Arguments of the merged-projection form, validated; tokens == 0 leaves *a untouched
+int qkv_rope_args(RopeArgs *a, void *qkv, int32_t tokens, int32_t heads, int32_t head_dim, int64_t row_stride,
+                  const void *q_weight, const void *k_weight, const void *cos_sin, int64_t cos_sin_stride,
+                  int64_t cos_sin_rows, int32_t rotary_dim, const int64_t *positions, float eps, const char *what) {
   if (head_dim != 64 && head_dim != 128)
     return set_error(TMHD_ERR_UNSUPPORTED, "%s: head_dim %d (64 or 128)", what, head_dim);
   if (tokens < 0 || heads <= 0 || row_stride < (int64_t)3 * heads * head_dim)
@@ -244,10 +273,64 @@ extern "C" int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int3
   if (rotary_dim && (!cos_sin || !positions || !aligned8(cos_sin) || cos_sin_stride % 4 ||
                      cos_sin_stride < rotary_dim || cos_sin_rows <= 0))
     return set_error(TMHD_ERR_INVALID, "%s: cos_sin must be 8-byte aligned rows of >= rotary_dim", what);
-  RopeArgs a{(const uint16_t *)qkv, (uint16_t *)qkv, row_stride, row_stride, (const uint16_t *)q_weight,
-             (const uint16_t *)k_weight, (const uint16_t *)cos_sin, nullptr, cos_sin_stride, 0, positions,
-             cos_sin_rows, tokens, heads, 2, rotary_dim, eps};
+  *a = RopeArgs{(const uint16_t *)qkv, (uint16_t *)qkv, row_stride, row_stride, (const uint16_t *)q_weight,
+                (const uint16_t *)k_weight, (const uint16_t *)cos_sin, nullptr, cos_sin_stride, 0, positions,
+                cos_sin_rows, tokens, heads, 2, rotary_dim, eps, nullptr, 0, 0, 0, 0};
+  return rope_rows_check(*a, head_dim, what);
+}
+
+}  // namespace
+}  // namespace tmhd
+
+extern "C" int tmhd_qkv_norm_rope(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim, int64_t row_stride,
+                                  const void *q_weight, const void *k_weight, const void *cos_sin,
+                                  int64_t cos_sin_stride, int64_t cos_sin_rows, int32_t rotary_dim,
+                                  const int64_t *positions, float eps, void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_qkv_norm_rope";
+  RopeArgs a{};
+  if (int st = qkv_rope_args(&a, qkv, tokens, heads, head_dim, row_stride, q_weight, k_weight, cos_sin,
+                             cos_sin_stride, cos_sin_rows, rotary_dim, positions, eps, what))
+    return st;
+  if (tokens == 0) return TMHD_OK;
   return launch_rope(a, head_dim, true, stream, what);
+}
+
+extern "C" int tmhd_qkv_norm_rope_stage(void *qkv, int32_t tokens, int32_t heads, int32_t head_dim,
+                                        int64_t row_stride, const void *q_weight, const void *k_weight,
+                                        const void *cos_sin, int64_t cos_sin_stride, int64_t cos_sin_rows,
+                                        int32_t rotary_dim, const int64_t *positions, float eps, int32_t stage_row0,
+                                        int32_t stage_n, void *k_slot, void *vt_slot, int64_t k_head_stride,
+                                        int64_t vt_head_stride, int32_t vt_row_stride, int32_t dst, int32_t zero_to,
+                                        void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_qkv_norm_rope_stage";
+  RopeArgs a{};
+  if (int st = qkv_rope_args(&a, qkv, tokens, heads, head_dim, row_stride, q_weight, k_weight, cos_sin,
+                             cos_sin_stride, cos_sin_rows, rotary_dim, positions, eps, what))
+    return st;
+  if (stage_row0 < 0 || stage_n < 0 || (int64_t)stage_row0 + stage_n > tokens)
+    return set_error(TMHD_ERR_INVALID, "%s: staged rows [%d, %d) outside the %d tokens", what, stage_row0,
+                     stage_row0 + stage_n, tokens);
+  if ((uintptr_t)qkv % 16 || row_stride % 8)
+    return set_error(TMHD_ERR_INVALID, "%s: qkv rows must be 16-byte aligned", what);
+  uint16_t *const base = (uint16_t *)qkv;
+  const int64_t width = (int64_t)heads * head_dim;
+  // the slot arguments are those of tmhd_kv_pack over the K and V thirds (checked before any launch)
+  if (int st = kv_pack(base + width, base + 2 * width, row_stride, head_dim, nullptr, stage_row0, stage_n, k_slot,
+                       vt_slot, k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, heads, head_dim, stream,
+                       false, true))
+    return st;
+  if (tokens > 0) {
+    a.kslot = (uint16_t *)k_slot;
+    a.kslot_hs = k_head_stride;
+    a.stage_row0 = stage_row0;
+    a.stage_n = stage_n;
+    a.stage_dst = dst;
+    if (int st = launch_rope(a, head_dim, true, stream, what, true, stage_n > 0)) return st;
+  }
+  return kv_pack(base + width, base + 2 * width, row_stride, head_dim, nullptr, stage_row0, stage_n, k_slot, vt_slot,
+                 k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, heads, head_dim, stream, false, false);
 }
 
 extern "C" int tmhd_qk_norm_rope(const void *value, int32_t tokens, int32_t heads, int32_t head_dim,

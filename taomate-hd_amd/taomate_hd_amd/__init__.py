@@ -41,7 +41,7 @@ from .adaln import (
     fused_swiglu,
 )
 from .packed import packed_sdpa
-from .rope import fused_apply_rope, fused_qk_norm_rope, fused_qkv_qk_norm_rope_
+from .rope import fused_apply_rope, fused_qk_norm_rope, fused_qkv_qk_norm_rope_, fused_qkv_qk_norm_rope_stage_
 from .quant import (
     cutlass_scaled_mm,
     cutlass_scaled_mm_out,
@@ -76,6 +76,7 @@ __all__ = [
     "fused_swiglu",
     "packed_sdpa",
     "fused_qkv_qk_norm_rope_",
+    "fused_qkv_qk_norm_rope_stage_",
     "_native",
     "AVKV",
     "AUDIO_TOKEN_TAG",

@@ -131,6 +131,14 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             c_void_p, c_int64, c_int64, c_int32, c_void_p, c_float, c_void_p,
         ],
     ),
+    "tmhd_qkv_norm_rope_stage": (
+        c_int,
+        [
+            c_void_p, c_int32, c_int32, c_int32, c_int64, c_void_p, c_void_p,
+            c_void_p, c_int64, c_int64, c_int32, c_void_p, c_float,
+            c_int32, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_int32, c_int32, c_void_p,
+        ],
+    ),
     "tmhd_token_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_void_p]),
     "tmhd_weight_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "tmhd_gemm_w8a8": (

@@ -29,9 +29,11 @@ from __future__ import annotations
 from enum import Enum
 from typing import Any, Callable
 
+from . import _native
 from .attention import QKQuantWorkspace, segment_attention
 from .kvcache import HeadMajorRingKVCache
 from .profiling import ComponentTimer, maybe_region
+from .rope import fused_qkv_qk_norm_rope_stage_
 from .slots import SlotPool, SlotView
 
 ATTENTION_BACKENDS = ("sdpa", "sage_attn")
@@ -133,6 +135,7 @@ class StreamingAttentionHook:
         self._condition_attention_cached = condition_attention_cached
         self._compact_output = compact_condition_attention_output
         self._scratch: SlotPool | None = None
+        self._prestaged: dict[str, tuple[Any, tuple[int, ...], int, int]] = {}
         self._quant_ws: QKQuantWorkspace | None = None
         self.sage_attn_calls = 0
         self.sage_attn_query_tokens = 0
@@ -202,12 +205,44 @@ class StreamingAttentionHook:
         self._live_document_rows = {}
         self._staged_match = {}
 
+    # ---- pre-staging (no counterpart in the reference)
+    def preprocess_qkv_(self, layer_name: str, qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any,
+                        positions: Any, eps: float, *, row0: int, count: int) -> Any:
+        """``fused_qkv_qk_norm_rope_`` of a layer's merged projection that also
+        packs the K/V of tokens ``row0 .. row0 + count`` into a scratch slot.
+
+        The next call of this hook for ``layer_name`` reads that slot in place
+        of packing, when the K/V it receives are the K and V thirds of this
+        ``qkv`` and the rows it would pack are exactly these (the media rows
+        of the live document in the noisy and fused-progress modes); any
+        other rows are packed as usual, and the slot is recycled after that
+        call either way.  Returns ``qkv``.
+        """
+        import torch
+
+        if layer_name not in self.cache.contract.layer_names:
+            raise ValueError(f"streaming hook reached a non-main attention layer: {layer_name}")
+        heads, head_dim = self.cache.contract.local_heads, self.cache.contract.head_dim
+        pool = self._pool(torch, qkv.device, heads, head_dim)
+        stale = self._prestaged.pop(layer_name, None)
+        if stale is not None:
+            pool.release(stale[0])
+        slot = pool.acquire(int(count))
+        try:
+            fused_qkv_qk_norm_rope_stage_(qkv, q_weight, k_weight, cos_sin_cache, positions, eps, slot,
+                                          row0=int(row0), count=int(count))
+        except BaseException:
+            pool.release(slot)
+            raise
+        width = heads * head_dim
+        key_at = (_native.ptr(qkv) + 2 * width, _native.ptr(qkv) + 4 * width, int(qkv.stride(0)))
+        self._prestaged[layer_name] = (slot, key_at, int(row0), int(count))
+        return qkv
+
     # ---- helpers
-    def _pool(self, torch: Any, query: Any) -> SlotPool:
-        if self._scratch is None or self._scratch.device != query.device:
-            self._scratch = SlotPool(
-                torch, heads=int(query.shape[1]), head_dim=int(query.shape[2]), device=query.device
-            )
+    def _pool(self, torch: Any, device: Any, heads: int, head_dim: int) -> SlotPool:
+        if self._scratch is None or self._scratch.device != device:
+            self._scratch = SlotPool(torch, heads=int(heads), head_dim=int(head_dim), device=device)
         return self._scratch
 
     def _attend(self, torch: Any, query: Any, q_rows: _Rows, views: list[SlotView], out: Any, scale: float) -> None:
@@ -313,10 +348,21 @@ class StreamingAttentionHook:
         live_document = live_documents[-1]
         previous_live_document = live_documents[0] if fused else None
         scale = float(attention.softmax_scale)
-        pool = self._pool(torch, query)
+        pool = self._pool(torch, query.device, int(query.shape[1]), int(query.shape[2]))
         acquired: list[Any] = []
+        prestaged = self._prestaged.pop(layer_name, None)
+        if prestaged is not None:
+            acquired.append(prestaged[0])
+            at = (_native.ptr(key), _native.ptr(value), int(key.stride(0)))
+            if at != prestaged[1] or key.stride(1) != int(key.shape[2]):
+                prestaged = None
 
         def scratch_pack(rows: _Rows) -> SlotView:
+            nonlocal prestaged
+            if prestaged is not None and rows.index is None and (rows.start, rows.count) == prestaged[2:]:
+                view = prestaged[0].view()
+                prestaged = None  # one use
+                return view
             slot = pool.acquire(rows.count)
             acquired.append(slot)
             with maybe_region(self.timer, "pack"):

@@ -1,6 +1,7 @@
 """Q/K RMSNorm + RoPE in front of the hook.
 
-``fused_qkv_qk_norm_rope_`` (in place in the merged QKV projection),
+``fused_qkv_qk_norm_rope_`` (in place in the merged QKV projection; the
+``_stage_`` form also writes the chunk's K/V into a cache slot),
 ``fused_qk_norm_rope`` (one projection, new output) and ``fused_apply_rope``
 (the rotation alone) have the reference's signatures, checks and error
 messages (src/taomate_hd/inference/fused_kernels.py:673-692, 798-873) and
@@ -19,16 +20,8 @@ from typing import Any
 from . import _native
 
 
-def fused_qkv_qk_norm_rope_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any, positions: Any, eps: float) -> Any:
-    """Normalize and rotate Q/K in place in a merged bf16 QKV projection.
-
-    ``qkv`` is ``[tokens, 3 * heads * head_dim]`` (Q, K, V); V is not read or
-    written.  ``cos_sin_cache`` is ``[positions, rotary_dim]`` bf16 (cos in the
-    first half of a row, sin in the second) and ``positions`` holds one
-    position per token.  Returns ``qkv``.
-    """
-    import torch
-
+def _merged_qkv_args(torch: Any, qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any, positions: Any):
+    """The reference's checks of the merged-projection form (fused_kernels.py:824-873)."""
     if qkv.ndim != 2 or not qkv.is_contiguous():
         raise ValueError("fused QKV preprocessing requires contiguous [tokens, width]")
     if q_weight.shape != k_weight.shape or q_weight.ndim != 1:
@@ -51,14 +44,60 @@ def fused_qkv_qk_norm_rope_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cach
     for name, t in (("qkv", qkv), ("q_weight", q_weight), ("k_weight", k_weight), ("cos_sin_cache", cache)):
         if t.device != qkv.device or t.device.type != "cuda":
             raise ValueError(f"{name} must be on the GPU of qkv")
-    q_weight = q_weight.contiguous()
-    k_weight = k_weight.contiguous()
+    return tokens, heads, head_dim, positions, cache, rotary_dim, q_weight.contiguous(), k_weight.contiguous()
+
+
+def fused_qkv_qk_norm_rope_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any, positions: Any, eps: float) -> Any:
+    """Normalize and rotate Q/K in place in a merged bf16 QKV projection.
+
+    ``qkv`` is ``[tokens, 3 * heads * head_dim]`` (Q, K, V); V is not read or
+    written.  ``cos_sin_cache`` is ``[positions, rotary_dim]`` bf16 (cos in the
+    first half of a row, sin in the second) and ``positions`` holds one
+    position per token.  Returns ``qkv``.
+    """
+    import torch
+
+    tokens, heads, head_dim, positions, cache, rotary_dim, q_weight, k_weight = _merged_qkv_args(
+        torch, qkv, q_weight, k_weight, cos_sin_cache, positions)
     status = _native.load().tmhd_qkv_norm_rope(
         _native.ptr(qkv), tokens, heads, head_dim, qkv.stride(0), _native.ptr(q_weight), _native.ptr(k_weight),
         _native.ptr(cache), cache.stride(0), int(cache.shape[0]), rotary_dim, _native.ptr(positions), float(eps),
         _native.stream_ptr(torch, qkv.device),
     )
     _native.check(status, "tmhd_qkv_norm_rope")
+    return qkv
+
+
+def fused_qkv_qk_norm_rope_stage_(qkv: Any, q_weight: Any, k_weight: Any, cos_sin_cache: Any, positions: Any,
+                                  eps: float, slot: Any, *, row0: int = 0, count: int | None = None,
+                                  dst: int = 0) -> Any:
+    """``fused_qkv_qk_norm_rope_`` that also stages the chunk: the K and V of
+    tokens ``row0 .. row0 + count`` land in ``slot`` (a ``KVSlot``) at rows
+    ``dst ..``, exactly as ``slot.pack(k, v, row0=row0, count=count, dst=dst)``
+    of the processed projection would put them, without a separate pass over
+    K.  Returns ``qkv``."""
+    import torch
+
+    from .slots import KV_TILE, round_up
+
+    tokens, heads, head_dim, positions, cache, rotary_dim, q_weight, k_weight = _merged_qkv_args(
+        torch, qkv, q_weight, k_weight, cos_sin_cache, positions)
+    if (slot.heads, slot.head_dim) != (heads, head_dim) or slot.device != qkv.device:
+        raise ValueError(f"slot {(slot.heads, slot.head_dim)} on {slot.device} does not take this projection's K/V")
+    n = tokens - int(row0) if count is None else int(count)
+    if int(row0) < 0 or n < 0 or int(row0) + n > tokens:
+        raise ValueError(f"rows [{row0}, {int(row0) + n}) outside the {tokens} tokens")
+    dst = int(dst)
+    if dst < 0 or dst % KV_TILE or dst + n > slot.capacity:
+        raise ValueError(f"{n} rows at slot row {dst} do not fit the slot capacity {slot.capacity} (tile-aligned)")
+    status = _native.load().tmhd_qkv_norm_rope_stage(
+        _native.ptr(qkv), tokens, heads, head_dim, qkv.stride(0), _native.ptr(q_weight), _native.ptr(k_weight),
+        _native.ptr(cache), cache.stride(0), int(cache.shape[0]), rotary_dim, _native.ptr(positions), float(eps),
+        int(row0), n, _native.ptr(slot.k), _native.ptr(slot.vt), slot.capacity * head_dim, slot.capacity * head_dim,
+        slot.capacity, dst, dst + round_up(n, KV_TILE), _native.stream_ptr(torch, qkv.device),
+    )
+    _native.check(status, "tmhd_qkv_norm_rope_stage")
+    slot.tokens = dst + n
     return qkv
 
 

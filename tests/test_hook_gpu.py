@@ -241,3 +241,54 @@ def test_session_rollback_on_error(torch_mod, dev):
                              token_tags=torch.tensor(tags, device=dev), commit_mask=torch.tensor(mask, device=dev),
                              cu_seqlens=None, cu_seqlens_host=bounds, max_seqlen=T)
         assert cache.committed_blocks == 0 and not cache.clean_commit_active
+
+
+def test_prestaged_chunk_used_without_pack(torch_mod, dev, monkeypatch):
+    """preprocess_qkv_ (norm + RoPE that also stages the media rows) followed
+    by the hook gives the same output, bit for bit, as norm + RoPE then the
+    hook, and the hook packs one segment fewer."""
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook, fused_qkv_qk_norm_rope_
+    from taomate_hd_amd import slots as slots_mod
+    from taomate_hd_amd.hook import HookMode
+
+    packs = []
+    orig = slots_mod.KVSlot.pack
+
+    def counting_pack(self, *a, **kw):
+        packs.append(1)
+        return orig(self, *a, **kw)
+
+    monkeypatch.setattr(slots_mod.KVSlot, "pack", counting_pack)
+    tags, mask, bounds = ost.packed_layout(37, 20, 14, 90)
+    T, width = len(tags), H * D
+    media0, media_n = 37 + 20, 14 + 90
+    rng = np.random.default_rng(3)
+    qkv = bf16.round_f32(rng.standard_normal((T, 3 * width)).astype(np.float32))
+    w = bf16.to_torch(bf16.round_f32(1.0 + 0.1 * rng.standard_normal(D).astype(np.float32)), dev)
+    ang = rng.uniform(-4, 4, (T, 48))
+    cs = bf16.to_torch(bf16.round_f32(np.concatenate([np.cos(ang), np.sin(ang)], -1).astype(np.float32)), dev)
+    pos = torch.arange(T, device=dev)
+    outs, counts = [], []
+    for prestage in (False, True):
+        cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
+        hook = StreamingAttentionHook(cache)
+        hook.activate(mode=HookMode.NOISY, block_index=0)
+        t = bf16.to_torch(qkv, dev)
+        if prestage:
+            hook.preprocess_qkv_(LAYERS[0], t, w, w, cs, pos, 1e-6, row0=media0, count=media_n)
+        else:
+            fused_qkv_qk_norm_rope_(t, w, w, cs, pos, 1e-6)
+        del packs[:]
+        q, k, v = (t[:, i * width : (i + 1) * width].view(T, H, D) for i in range(3))
+        out = hook(attention=_Attn(), layer_name=LAYERS[0], query=q, key=k, value=v,
+                   token_tags=torch.tensor(tags, device=dev), commit_mask=torch.tensor(mask, device=dev),
+                   cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=tuple(bounds),
+                   max_seqlen=T)
+        torch.cuda.synchronize()
+        outs.append(out.clone())
+        counts.append(len(packs))
+        assert not hook._prestaged  # consumed by the call
+        hook.deactivate()
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert counts[1] == counts[0] - 1

@@ -163,3 +163,45 @@ def test_apply_rope_bit_exact(torch_mod, dev, tokens, heads, head_dim, rotary):
     torch.cuda.synchronize()
     want = orope.apply_rope(qkv[:, :width].reshape(tokens, heads, head_dim), cos, sin)
     assert np.array_equal(bf16.from_torch(out).view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize(
+    "tokens,heads,head_dim,rotary,row0,count,dst",
+    [(200, 3, 128, 96, 37, 130, 64), (64, 2, 128, 128, 0, 64, 0), (90, 4, 64, 40, 5, 0, 0), (150, 2, 64, 64, 20, 77, 128),
+     (33, 5, 128, 0, 0, 33, 0)],
+)
+def test_qkv_norm_rope_stage_equals_norm_rope_then_pack(torch_mod, dev, tokens, heads, head_dim, rotary, row0, count,
+                                                        dst):
+    """The staged form leaves the projection and the whole slot (data rows,
+    zeroed tail, untouched rows) bit-identical to norm + RoPE followed by
+    KVSlot.pack of the same rows."""
+    torch = torch_mod
+    from taomate_hd_amd import fused_qkv_qk_norm_rope_, fused_qkv_qk_norm_rope_stage_
+    from taomate_hd_amd.slots import KVSlot
+
+    qkv, qw, kw, cache, pos = _case(tokens, heads, head_dim, rotary, seed=tokens + count, npos=tokens)
+    args = (bf16.to_torch(qw, dev), bf16.to_torch(kw, dev), bf16.to_torch(cache, dev).reshape(cache.shape[0], rotary),
+            torch.tensor(pos, device=dev), 1e-6)
+    slots = []
+    for _ in range(2):
+        s = KVSlot(torch, heads=heads, head_dim=head_dim, capacity=dst + count + 130, device=dev)
+        g = torch.Generator(device=dev).manual_seed(5)
+        s.k.copy_(torch.randn(s.k.shape, generator=g, device=dev).to(torch.bfloat16))  # stale contents
+        s.vt.copy_(torch.randn(s.vt.shape, generator=g, device=dev).to(torch.bfloat16))
+        slots.append(s)
+    a = bf16.to_torch(qkv, dev)
+    b = a.clone()
+    width = heads * head_dim
+    fused_qkv_qk_norm_rope_(a, *args)
+    view = lambda t, i: t[:, i * width : (i + 1) * width].view(tokens, heads, head_dim)  # noqa: E731
+    slots[0].pack(view(a, 1), view(a, 2), row0=row0, count=count, dst=dst)
+    out = fused_qkv_qk_norm_rope_stage_(b, *args, slots[1], row0=row0, count=count, dst=dst)
+    torch.cuda.synchronize()
+    assert out is b and slots[1].tokens == slots[0].tokens == dst + count
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    assert torch.equal(slots[0].k.view(torch.int16), slots[1].k.view(torch.int16))
+    assert torch.equal(slots[0].vt.view(torch.int16), slots[1].vt.view(torch.int16))
+    want = orope.qkv_norm_rope(qkv, qw, kw, cache, pos, 1e-6, heads)
+    assert np.array_equal(bf16.from_torch(b).view(np.uint32), want.view(np.uint32))
+    with pytest.raises(ValueError, match="outside the"):
+        fused_qkv_qk_norm_rope_stage_(b, *args, slots[1], row0=tokens - 1, count=2)
