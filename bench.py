@@ -228,6 +228,39 @@ def bench_mlp(torch, dev, steps, warmup):
     return {"two_step": two_ms, "fused": fused_ms}
 
 
+def bench_prep_hook(torch, dev, steps, warmup, cache, inputs):
+    """Q/K norm + RoPE of the chunk's merged projection, then the BF16 hook
+    layer call on the 768p cache: the chunk packed by the hook (norm + RoPE in
+    place, then the hook's pack) against the chunk staged by the norm + RoPE
+    kernel (hook.preprocess_qkv_).  Returns {name: device ms per step}."""
+    from taomate_hd_amd import HookMode, StreamingAttentionHook, fused_qkv_qk_norm_rope_
+
+    gen = torch.Generator(device=dev).manual_seed(12)
+    qkv = torch.cat([inputs[n].reshape(LQ, H * D) for n in ("query", "key", "value")], 1).contiguous()
+    w = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
+    ang = _randn(torch, (4096, ROTARY // 2), gen, dev)
+    table = torch.cat([ang.cos(), ang.sin()], -1).to(torch.bfloat16)
+    pos = torch.arange(LQ, device=dev) % 4096
+    views = {n: qkv[:, i * H * D : (i + 1) * H * D].view(LQ, H, D) for i, n in enumerate(("query", "key", "value"))}
+    args = dict(inputs, **views)
+    cu = torch.tensor([0, LQ], dtype=torch.int32, device=dev)
+    hook = StreamingAttentionHook(cache)
+    hook.activate(mode=HookMode.NOISY, block_index=cache.committed_blocks)
+
+    def packed_by_hook():
+        fused_qkv_qk_norm_rope_(qkv, w, w, table, pos, 1e-6)
+        hook_step(hook, args, cu)
+
+    def staged_by_rope():
+        hook.preprocess_qkv_(LAYER, qkv, w, w, table, pos, 1e-6, row0=0, count=LQ)
+        hook_step(hook, args, cu)
+
+    _, a_ms = time_steps(torch, packed_by_hook, steps, warmup)
+    _, b_ms = time_steps(torch, staged_by_rope, steps, warmup)
+    hook.deactivate()
+    return {"packed_by_hook": a_ms, "staged_by_rope": b_ms}
+
+
 def bench_rope(torch, dev, steps, warmup):
     """Q/K RMSNorm + RoPE in place in the merged QKV projection of the 768p chunk
     (the step in front of the hook), synthetic bf16 inputs; returns ms per call."""
@@ -336,7 +369,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "copy"),
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep", "copy"),
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -399,7 +432,7 @@ def main() -> int:
         print(json.dumps(result), flush=True)
         return 0
     cache = inputs = None
-    if args.workload in ("all", "bf16", "i8qk"):
+    if args.workload in ("all", "bf16", "i8qk", "prep"):
         cache, inputs = build_stream(torch, dev, None)
         torch.cuda.synchronize()
     if args.workload in ("all", "bf16"):
@@ -434,6 +467,19 @@ def main() -> int:
                 "speedup_of_value": round(ref_ms / wall_ms, 2),
             }
             _log(f"reference backend on this GPU: {ref_ms:.3f} ms per layer call")
+    if args.workload in ("all", "prep"):
+        prep = bench_prep_hook(torch, dev, args.steps, args.warmup, cache, inputs)
+        result["norm_rope_and_layer_call"] = {
+            "packed_by_hook_ms": round(prep["packed_by_hook"], 4),
+            "staged_by_rope_ms": round(prep["staged_by_rope"], 4),
+            "saving_us": round((prep["packed_by_hook"] - prep["staged_by_rope"]) * 1e3, 1),
+            "shape": f"merged QKV {LQ} x {3 * H * D}, rotary {ROTARY}, then the BF16 layer call over Lkv {LKV}",
+        }
+        _log(f"norm+rope then layer call: packed by hook {prep['packed_by_hook']:.3f} ms, "
+             f"staged by rope {prep['staged_by_rope']:.3f} ms")
+        if result["value"] is None:
+            result["value"] = round(ATTN_FLOPS / (prep["staged_by_rope"] * 1e-3) / 1e12, 2)
+            result["ms_per_step"] = round(prep["staged_by_rope"], 4)
     if args.workload in ("all", "i8qk"):
         wall_ms, dev_ms, comps = bench_attention(torch, dev, "sage_attn", args.steps, args.warmup, cache, inputs)
         tflops = ATTN_FLOPS / (wall_ms * 1e-3) / 1e12
