@@ -53,6 +53,9 @@ ATTN_FLOPS = 4.0 * H * LQ * LKV * D
 LAYER = "blocks.0.attn"
 M_X, K_X, N_W = 12252, 5120, 13824
 FFN = 14336  # MLP width of the DiT (model/architecture.py:21)
+# the model's own 768p HIGH-stage hook call: 14 local heads (56 over TP2 x Ulysses 2),
+# chunk = 10 latents x 1,032 video tokens + 2 x 57 audio, sink = 12 latents of video
+FAITHFUL = dict(heads=14, anchor=12 * 1032, video=10 * 1032, audio=2 * 57)
 TRAFFIC_PROFILE = REPO / "profiles" / "attn_fwd_bf16_768p_pmc.txt"
 
 
@@ -69,10 +72,11 @@ def _randn(torch, shape, gen, dev, std=1.0):
     return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std
 
 
-def build_stream(torch, dev, timer):
+def build_stream(torch, dev, timer, heads=H, anchor=ANCHOR, video=VIDEO, audio=AUDIO):
     """A cache holding the 768p anchor + two history chunks, and one chunk's inputs."""
     from taomate_hd_amd import HeadMajorRingKVCache, KVContract
 
+    H = heads  # noqa: N806 (the shapes below are per local head)
     gen = torch.Generator(device=dev).manual_seed(0)
     offset = _randn(torch, (H, D), gen, dev, 0.5)
     contract = KVContract(layer_names=(LAYER,), local_heads=H, head_dim=D)
@@ -89,21 +93,22 @@ def build_stream(torch, dev, timer):
         return q, k, v, tags, torch.ones(n, dtype=torch.bool, device=dev)
 
     # block 0 becomes the video-only anchor once two newer blocks exist
-    for block, (nv, na) in enumerate([(ANCHOR, AUDIO), (VIDEO, AUDIO), (VIDEO, AUDIO)]):
+    for block, (nv, na) in enumerate([(anchor, audio), (video, audio), (video, audio)]):
         _, k, v, tags, mask = chunk(nv, na)
         cache.begin_clean_commit(block)
         cache.stage(LAYER, k, v, tags, mask)
         cache.commit()
         cache.retain_sink_and_recent_commits(2)
-    assert cache.history_tokens == ANCHOR + 2 * LQ, cache.history_tokens
-    q, k, v, tags, mask = chunk(VIDEO, AUDIO)
+    assert cache.history_tokens == anchor + 2 * (video + audio), cache.history_tokens
+    q, k, v, tags, mask = chunk(video, audio)
     inputs = dict(query=q, key=k, value=v, token_tags=tags, commit_mask=mask)
     return cache, inputs
 
 
 def hook_step(hook, inputs, cu):
+    lq = int(inputs["query"].shape[0])
     return hook(
-        attention=_Attn(), layer_name=LAYER, cu_seqlens=cu, cu_seqlens_host=(0, LQ), max_seqlen=LQ, **inputs
+        attention=_Attn(), layer_name=LAYER, cu_seqlens=cu, cu_seqlens_host=(0, lq), max_seqlen=lq, **inputs
     )
 
 
@@ -130,7 +135,7 @@ def bench_attention(torch, dev, backend, steps, warmup, cache, inputs):
     timer = ComponentTimer(torch)
     hook = StreamingAttentionHook(cache, attention_backend=backend, timer=timer)
     hook.activate(mode=HookMode.NOISY, block_index=cache.committed_blocks)
-    cu = torch.tensor([0, LQ], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, int(inputs["query"].shape[0])], dtype=torch.int32, device=dev)
     out = None
 
     def step():
@@ -369,7 +374,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep", "copy"),
+    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep", "faithful", "copy"),
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -500,6 +505,25 @@ def main() -> int:
             result["value"], result["ms_per_step"] = round(tflops, 2), round(wall_ms, 4)
     if cache is not None:
         del cache, inputs
+        torch.cuda.empty_cache()
+    if args.workload in ("all", "faithful"):
+        fc, fi = build_stream(torch, dev, None, **FAITHFUL)
+        lq = FAITHFUL["video"] + FAITHFUL["audio"]
+        lkv = FAITHFUL["anchor"] + 3 * lq
+        flops = 4.0 * FAITHFUL["heads"] * lq * lkv * D
+        f_out = {}
+        for backend, name in (("sdpa", "bf16"), ("sage_attn", "i8qk")):
+            wall_ms, _, comps = bench_attention(torch, dev, backend, args.steps, args.warmup, fc, fi)
+            f_out[name] = {"ms_per_layer_call": round(wall_ms, 4),
+                           "tflops": round(flops / (wall_ms * 1e-3) / 1e12, 1),
+                           "components_ms": {k: round(v["mean_ms"], 4) for k, v in comps.items()}}
+            _log(f"faithful {name}: {wall_ms:.3f} ms per layer call")
+        f_out["shape"] = (f"model-faithful 768p HIGH hook call: H {FAITHFUL['heads']}, D {D}, Lq {lq} over Lkv {lkv} = "
+                          f"sink {FAITHFUL['anchor']} + 2 x {lq} history + {lq} self (text rows not included)")
+        result["model_faithful_768p"] = f_out
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = f_out["bf16"]["tflops"], f_out["bf16"]["ms_per_layer_call"]
+        del fc, fi
         torch.cuda.empty_cache()
     if args.workload in ("all", "w8a8"):
         wall_ms, w8_dev_ms, comps = bench_w8a8(torch, dev, args.steps, args.warmup)
