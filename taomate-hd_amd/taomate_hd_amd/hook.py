@@ -194,6 +194,10 @@ class StreamingAttentionHook:
         self._staged_match = {}
 
     def deactivate(self) -> None:
+        for slot, *_ in self._prestaged.values():  # staged but never consumed
+            if self._scratch is not None and slot.device == self._scratch.device:
+                self._scratch.release(slot)
+        self._prestaged = {}
         self.mode = HookMode.IDLE
         self.block_index = None
         self.fused_current_use_sink = None
@@ -225,7 +229,7 @@ class StreamingAttentionHook:
         heads, head_dim = self.cache.contract.local_heads, self.cache.contract.head_dim
         pool = self._pool(torch, qkv.device, heads, head_dim)
         stale = self._prestaged.pop(layer_name, None)
-        if stale is not None:
+        if stale is not None and stale[0].device == pool.device:
             pool.release(stale[0])
         slot = pool.acquire(int(count))
         try:
@@ -352,10 +356,13 @@ class StreamingAttentionHook:
         acquired: list[Any] = []
         prestaged = self._prestaged.pop(layer_name, None)
         if prestaged is not None:
-            acquired.append(prestaged[0])
-            at = (_native.ptr(key), _native.ptr(value), int(key.stride(0)))
-            if at != prestaged[1] or key.stride(1) != int(key.shape[2]):
-                prestaged = None
+            if prestaged[0].device != query.device:
+                prestaged = None  # staged on another GPU: dropped, never pooled here
+            else:
+                acquired.append(prestaged[0])
+                at = (_native.ptr(key), _native.ptr(value), int(key.stride(0)))
+                if at != prestaged[1] or key.stride(1) != int(key.shape[2]):
+                    prestaged = None
 
         def scratch_pack(rows: _Rows) -> SlotView:
             nonlocal prestaged

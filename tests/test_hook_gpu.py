@@ -292,3 +292,9 @@ def test_prestaged_chunk_used_without_pack(torch_mod, dev, monkeypatch):
         hook.deactivate()
     assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
     assert counts[1] == counts[0] - 1
+    # staged but never consumed: recycled by deactivate
+    hook.activate(mode=HookMode.NOISY, block_index=0)
+    hook.preprocess_qkv_(LAYERS[0], bf16.to_torch(qkv, dev), w, w, cs, pos, 1e-6, row0=media0, count=media_n)
+    slot = hook._prestaged[LAYERS[0]][0]
+    hook.deactivate()
+    assert not hook._prestaged and any(f is slot for f in hook._scratch._free)

@@ -264,3 +264,26 @@ def test_swiglu_row_interleave_layout_without_gpu():
     assert interleave_swiglu_rows(rows).tolist() == want  # 1-D (bias, scale vectors) too
     with pytest.raises(ValueError, match="multiple of 256"):
         interleave_swiglu_rows(torch.arange(2 * 200))
+
+
+def test_staged_norm_rope_validation_without_gpu():
+    import torch
+    from taomate_hd_amd import (HeadMajorRingKVCache, KVContract, StreamingAttentionHook,
+                                fused_qkv_qk_norm_rope_stage_)
+    from taomate_hd_amd.hook import HookMode
+
+    qkv = torch.zeros((8, 3 * 2 * 64), dtype=torch.bfloat16)
+    w = torch.ones(64, dtype=torch.bfloat16)
+    table = torch.zeros((8, 32), dtype=torch.bfloat16)
+    pos = torch.arange(8)
+    with pytest.raises(ValueError, match="three complete projections"):
+        fused_qkv_qk_norm_rope_stage_(qkv[:, :-64].contiguous(), w, w, table, pos, 1e-6, None)
+    with pytest.raises(ValueError, match="must be on the GPU"):  # checked before the slot is touched
+        fused_qkv_qk_norm_rope_stage_(qkv, w, w, table, pos, 1e-6, None)
+    hook = StreamingAttentionHook(HeadMajorRingKVCache(KVContract(layer_names=("blocks.0.attn",), local_heads=2,
+                                                                  head_dim=64)))
+    hook.activate(mode=HookMode.NOISY, block_index=0)
+    with pytest.raises(ValueError, match="non-main attention layer"):
+        hook.preprocess_qkv_("blocks.9.attn", qkv, w, w, table, pos, 1e-6, row0=0, count=8)
+    hook.deactivate()
+    assert hook._prestaged == {}
