@@ -93,33 +93,58 @@ __device__ __forceinline__ int64_t to_fixed(float x) {
   return (int64_t)__builtin_rintf(y);
 }
 
+// Key segments of one launch: workgroups [blk0[i], blk0[i + 1]) of the grid's
+// x dimension cover segment i (its own tokens, 256 per workgroup for the sums,
+// TMHD_QUANT_BLOCK for the blocks).
+struct KeySegs {
+  const uint16_t *k[kMaxSeg];
+  int64_t khs[kMaxSeg];
+  int8_t *q8[kMaxSeg];
+  int64_t q8hs[kMaxSeg];
+  float *qs[kMaxSeg];
+  int32_t qshs[kMaxSeg];
+  int32_t tokens[kMaxSeg];
+  int32_t blk0[kMaxSeg + 1];
+  int32_t n;
+};
+
+__device__ __forceinline__ int key_seg(const KeySegs &a, int b) {
+  int s = 0;
+  while (s + 1 < a.n && b >= a.blk0[s + 1]) ++s;
+  return s;
+}
+
 // Fixed-point column sums of one head's keys over 256 tokens per workgroup.
 // Thread (c, r) reads 16-byte chunk c (8 channels) of rows t0 + r, t0 + r + RPI, ...
-// and keeps 8 int64 partial sums; partials are combined in LDS and added to
-// ws[h][d] with one 64-bit atomic per channel.  Values with |x| < 127 take the
-// int32 conversion path; a chunk holding a larger value takes the int64 path
-// (both give rint(x * 2^24) exactly).
+// (all its loads issued before any is used) and keeps 8 int64 partial sums;
+// partials are combined in LDS and added to ws[h][d] with one 64-bit atomic per
+// channel.  Values with |x| < 127 take the int32 conversion path; a chunk
+// holding a larger value takes the int64 path (both give rint(x * 2^24) exactly).
 template <int D>
-__global__ void __launch_bounds__(256) k_sum_kernel(const uint16_t *__restrict__ k, int64_t khs, int32_t tokens,
-                                                    int64_t *__restrict__ ws) {
+__global__ void __launch_bounds__(256) k_sum_kernel(const KeySegs a, int64_t *__restrict__ ws) {
   constexpr int CPR = D / 8;      // 16-byte chunks per row
   constexpr int RPI = 256 / CPR;  // rows per pass
+  constexpr int NP = 256 / RPI;   // passes per workgroup
   __shared__ long long part[RPI][D];
   const int h = blockIdx.y, tid = threadIdx.x, c = tid % CPR, r = tid / CPR;
-  const int t0 = blockIdx.x * 256;
-  const int t1 = min(t0 + 256, tokens);
-  const uint16_t *base = k + (int64_t)h * khs + c * 8;
+  const int sg = key_seg(a, blockIdx.x);
+  const int t0 = (blockIdx.x - a.blk0[sg]) * 256;
+  const int n = min(a.tokens[sg] - t0, 256);
+  const uint16_t *base = a.k[sg] + (int64_t)h * a.khs[sg] + (int64_t)t0 * D + c * 8;
+  i32x4 raw[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) raw[p] = p * RPI + r < n ? *(const i32x4 *)(base + (int64_t)(p * RPI + r) * D) : i32x4{};
   long long acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0;
-  for (int t = t0 + r; t < t1; t += RPI) {
-    const i32x4 raw = *(const i32x4 *)(base + (int64_t)t * D);
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
     float x[8];
     float mx = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      x[2 * e] = bf16_bits_to_f32((uint32_t)raw[e] & 0xffffu);
-      x[2 * e + 1] = bf16_bits_to_f32((uint32_t)raw[e] >> 16);
+      x[2 * e] = bf16_bits_to_f32((uint32_t)raw[p][e] & 0xffffu);
+      x[2 * e + 1] = bf16_bits_to_f32((uint32_t)raw[p][e] >> 16);
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(x[e]));
@@ -157,16 +182,16 @@ __global__ void k_mean_finalize_kernel(const int64_t *__restrict__ ws, uint16_t 
 // Rows in [nvalid, nwrite) are written as zero; every launched block writes
 // its scale (0 for a block without valid rows).
 template <int D>
-__global__ void __launch_bounds__(256) block_quant_kernel(const uint16_t *__restrict__ src, int64_t sts, int64_t shs,
-                                                          const int32_t *__restrict__ rows, int32_t row0,
-                                                          const uint16_t *__restrict__ mean, int32_t nvalid,
-                                                          int32_t nwrite, int8_t *__restrict__ q8, int64_t q8hs,
-                                                          float *__restrict__ qscale, int32_t qshs) {
+__device__ __forceinline__ void quant_block(const uint16_t *__restrict__ src, int64_t sts, int64_t shs,
+                                            const int32_t *__restrict__ rows, int32_t row0,
+                                            const uint16_t *__restrict__ mean, int32_t nvalid, int32_t nwrite,
+                                            int8_t *__restrict__ q8, int64_t q8hs, float *__restrict__ qscale,
+                                            int32_t qshs, int h, int blk) {
   constexpr int CPR = D / 8;          // 8-element chunks per row
   constexpr int RPI = 256 / CPR;      // rows per pass
   constexpr int NP = TMHD_QUANT_BLOCK / RPI;
   __shared__ float red[4];
-  const int h = blockIdx.y, blk = blockIdx.x, tid = threadIdx.x;
+  const int tid = threadIdx.x;
   const int ch = tid % CPR, r0 = tid / CPR;
   float mf[8];
 #pragma unroll
@@ -213,6 +238,25 @@ __global__ void __launch_bounds__(256) block_quant_kernel(const uint16_t *__rest
   }
 }
 
+template <int D>
+__global__ void __launch_bounds__(256) block_quant_kernel(const uint16_t *__restrict__ src, int64_t sts, int64_t shs,
+                                                          const int32_t *__restrict__ rows, int32_t row0,
+                                                          const uint16_t *__restrict__ mean, int32_t nvalid,
+                                                          int32_t nwrite, int8_t *__restrict__ q8, int64_t q8hs,
+                                                          float *__restrict__ qscale, int32_t qshs) {
+  quant_block<D>(src, sts, shs, rows, row0, mean, nvalid, nwrite, q8, q8hs, qscale, qshs, blockIdx.y, blockIdx.x);
+}
+
+// Every key segment's blocks in one launch (slot rows: token stride D); rows up
+// to the 64-token tile padding are written.
+template <int D>
+__global__ void __launch_bounds__(256) key_block_quant_kernel(const KeySegs a, const uint16_t *__restrict__ mean) {
+  const int sg = key_seg(a, blockIdx.x);
+  const int nwrite = (a.tokens[sg] + kTile - 1) / kTile * kTile;
+  quant_block<D>(a.k[sg], D, a.khs[sg], nullptr, 0, mean, a.tokens[sg], nwrite, a.q8[sg], a.q8hs[sg], a.qs[sg],
+                 a.qshs[sg], blockIdx.y, blockIdx.x - a.blk0[sg]);
+}
+
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 template <int D>
@@ -232,24 +276,34 @@ int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s
   int64_t total = 0;
   for (int i = 0; i < a->n_segments; ++i) total += a->seg[i].tokens;
   // 1. exact key sums, 2. bf16 mean
-  hipLaunchKernelGGL(zero_i64_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, H * D);
+  // one segment table for the key passes; workgroup ranges per pass
+  KeySegs ks{};
+  ks.n = a->n_segments;
   for (int i = 0; i < a->n_segments; ++i) {
     const tmhd_kv_segment &sg = a->seg[i];
-    hipLaunchKernelGGL(k_sum_kernel<D>, dim3((sg.tokens + 255) / 256, H), dim3(256), 0, s,
-                       (const uint16_t *)sg.k, sg.k_head_stride, sg.tokens, qq->mean_workspace);
+    ks.k[i] = (const uint16_t *)sg.k;
+    ks.khs[i] = sg.k_head_stride;
+    ks.q8[i] = qq->k_i8[i];
+    ks.q8hs[i] = qq->k_head_stride[i];
+    ks.qs[i] = qq->k_scale[i];
+    ks.qshs[i] = qq->k_scale_head_stride[i];
+    ks.tokens[i] = sg.tokens;
   }
+  auto ranges = [&](int per) {
+    ks.blk0[0] = 0;
+    for (int i = 0; i < ks.n; ++i) ks.blk0[i + 1] = ks.blk0[i] + (ks.tokens[i] + per - 1) / per;
+    return ks.blk0[ks.n];
+  };
+  hipLaunchKernelGGL(zero_i64_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, H * D);
+  const int nsum = ranges(256);
+  hipLaunchKernelGGL(k_sum_kernel<D>, dim3(nsum, H), dim3(256), 0, s, ks, qq->mean_workspace);
   hipLaunchKernelGGL(k_mean_finalize_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace,
                      qq->k_mean, H * D, (double)total);
   if (int st = check_launch("smooth-K mean")) return st;
-  // 3. keys, per segment (rows up to the 64-token tile padding are written)
-  for (int i = 0; i < a->n_segments; ++i) {
-    const tmhd_kv_segment &sg = a->seg[i];
-    const int nwrite = (sg.tokens + kTile - 1) / kTile * kTile;
-    if (int st = launch_block_quant<D>((const uint16_t *)sg.k, D, sg.k_head_stride, nullptr, 0, qq->k_mean,
-                                       sg.tokens, nwrite, qq->k_i8[i], qq->k_head_stride[i], qq->k_scale[i],
-                                       qq->k_scale_head_stride[i], H, s))
-      return st;
-  }
+  // 3. keys, every segment in one launch (rows up to the 64-token tile padding are written)
+  const int nblk = ranges(TMHD_QUANT_BLOCK);
+  hipLaunchKernelGGL(key_block_quant_kernel<D>, dim3(nblk, H), dim3(256), 0, s, ks, (const uint16_t *)qq->k_mean);
+  if (int st = check_launch("block_quant keys")) return st;
   // 4. queries (rows up to the 256-row workgroup padding are written)
   const int qcap = (a->lq + 255) / 256 * 256;
   return launch_block_quant<D>((const uint16_t *)a->q, a->q_token_stride, a->q_head_stride, a->q_rows, a->q_row0,
