@@ -287,3 +287,13 @@ def test_staged_norm_rope_validation_without_gpu():
         hook.preprocess_qkv_("blocks.9.attn", qkv, w, w, table, pos, 1e-6, row0=0, count=8)
     hook.deactivate()
     assert hook._prestaged == {}
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, str(REPO / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300, cwd=str(REPO))
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr and r.stdout == ""
