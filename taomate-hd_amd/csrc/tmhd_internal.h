@@ -57,13 +57,40 @@ __device__ __forceinline__ uint32_t pack_bf16_rne(float lo, float hi) {
 }
 
 // SwiGLU of one packed bf16 pair of gates and ups: R(R(g * sigmoid(g)) * u),
-// sigmoid(g) = 1 / (1 + exp(-g)) with the accurate single-precision exp and a
-// correctly rounded division (shared by the SwiGLU kernel and the GEMM's
-// fused SwiGLU epilogue, so both give the same bits).
+// sigmoid(g) = 1 / (1 + e^-g) in 12 instructions: e^-g = 2^t (1 + lo) with
+// t = -g * log2(e) rounded and lo its rounding residual (log2(e) split into a
+// float head and a tail, the residual of the head's product taken exactly with
+// an FMA: Cody and Waite's argument reduction), 2^t from v_exp_f32, then the
+// hardware reciprocal refined by one Newton step.  For every bf16 gate above
+// -87.5 the SwiGLU output equals that of the correctly rounded division of
+// 1 by 1 + expf(-g); below it both give outputs under 1e-36 in magnitude
+// (this form returns 0 there: the reciprocal flushes denormals).  The input is
+// clamped to [-128, 128] (NaN to -128), so that infinities and NaN never meet
+// the correction: +inf gives 1, -inf and NaN give 0, and g * sigmoid(g) is then
+// inf, NaN, NaN as with the division.
+__device__ __forceinline__ float sigmoid_f32(float g) {
+#pragma clang fp contract(off)
+  constexpr float kLog2eHi = 1.44269502162933349609375f;                      // log2(e) rounded to float
+  constexpr float kLog2eLoLn2 = 1.925963033500011e-08f * 0.6931471805599453f;  // (log2(e) - head) * ln 2
+  constexpr float kLn2 = 0.6931471805599453f;
+  const float gc = fminf(fmaxf(g, -128.0f), 128.0f);
+  const float t = gc * -kLog2eHi;
+  const float r1 = __builtin_fmaf(gc, -kLog2eHi, -t);            // exact: -gc * head - t
+  const float lo = __builtin_fmaf(r1, kLn2, gc * -kLog2eLoLn2);  // (-gc log2(e) - t) ln 2
+  float e = __builtin_amdgcn_exp2f(t);
+  e = __builtin_fmaf(e, lo, e);  // 2^t e^lo to first order
+  const float d = 1.0f + e;
+  const float r = __builtin_amdgcn_rcpf(d);
+  return fmaxf(__builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r), 0.0f);  // d = inf: NaN -> 0
+}
+
+// silu(gate) * up of two bf16 pairs, rounded as the reference rounds it
+// (shared by the SwiGLU kernel and the GEMM's fused SwiGLU epilogue, so both
+// give the same bits).
 __device__ __forceinline__ uint32_t swiglu_pair(uint32_t g, uint32_t u) {
 #pragma clang fp contract(off)
   const float g0 = __uint_as_float(g << 16), g1 = __uint_as_float(g & 0xffff0000u);
-  const float s0 = __fdiv_rn(1.0f, 1.0f + expf(-g0)), s1 = __fdiv_rn(1.0f, 1.0f + expf(-g1));
+  const float s0 = sigmoid_f32(g0), s1 = sigmoid_f32(g1);
   const uint32_t act = pack_bf16_rne(g0 * s0, g1 * s1);
   return pack_bf16_rne(__uint_as_float(act << 16) * __uint_as_float(u << 16),
                        __uint_as_float(act & 0xffff0000u) * __uint_as_float(u & 0xffff0000u));

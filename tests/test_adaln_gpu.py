@@ -102,3 +102,30 @@ def test_swiglu_within_one_bf16_ulp(torch_mod, dev, rows, half):
     ulps = np.abs((gi >> 16) - (wi >> 16))
     assert ulps.max() <= 1
     assert np.mean(ulps == 0) >= 0.999
+
+
+def test_swiglu_every_bf16_gate(torch_mod, dev):
+    """All 65,536 bf16 gate patterns against five up values: bit-identical to
+    the oracle (sigmoid in float64) wherever the gate is above -87.5; below it
+    the exact silu(gate) is under 1e-36 in magnitude and the kernel's output
+    may be a signed zero in place of the product; NaN gates give NaN."""
+    torch = torch_mod
+    from taomate_hd_amd import fused_swiglu
+
+    gates = np.arange(65536, dtype=np.uint32) << 16
+    g = np.tile(gates.view(np.float32), 5)
+    u = np.repeat(np.array([1.0, 1.5, -3.75, 0.0107, 100.0], dtype=np.float32), 65536)
+    u = bf16.round_f32(u)
+    x = np.concatenate([g.reshape(-1, 1024), u.reshape(-1, 1024)], 1)  # rows [gate 1024 | up 1024]
+    out = fused_swiglu(bf16.to_torch(x, dev).reshape(1, -1, 2048))
+    torch.cuda.synchronize()
+    got = bf16.from_torch(out).reshape(-1)
+    with np.errstate(over="ignore", invalid="ignore"):
+        want = oada.swiglu(x).reshape(-1)
+    nan_g = np.isnan(g)
+    assert np.all(np.isnan(got[nan_g]))
+    live = ~nan_g & ~(g <= -87.5)
+    assert np.array_equal(got[live].view(np.uint32), want[live].view(np.uint32))
+    deep = ~nan_g & (g <= -87.5) & np.isfinite(g)
+    bound = 1e-36 * np.maximum(1.0, np.abs(u[deep]))
+    assert np.all(np.abs(got[deep]) <= bound) and np.all(np.abs(want[deep]) <= bound)
