@@ -102,8 +102,8 @@ typedef struct tmhd_qk_quant {
   float *k_scale[TMHD_MAX_SEGMENTS];    /* [H][cap / 128] per segment */
   int64_t k_head_stride[TMHD_MAX_SEGMENTS];       /* elements */
   int32_t k_scale_head_stride[TMHD_MAX_SEGMENTS]; /* elements */
-  uint16_t *k_mean;             /* bf16 [H][D] written by tmhd_qk_smooth_quant */
-  int64_t *mean_workspace;      /* int64 [H][D] scratch */
+  uint16_t *k_mean;             /* bf16 [H][D] written by tmhd_qk_smooth_quant (16-byte aligned) */
+  int64_t *mean_workspace;      /* int64 [H][D] scratch (8-byte aligned) */
 } tmhd_qk_quant;
 
 /* Library identification: "tmhd <version> gfx950". */

@@ -131,9 +131,14 @@ __global__ void __launch_bounds__(256) k_sum_kernel(const KeySegs a, int64_t *__
   const int t0 = (blockIdx.x - a.blk0[sg]) * 256;
   const int n = min(a.tokens[sg] - t0, 256);
   const uint16_t *base = a.k[sg] + (int64_t)h * a.khs[sg] + (int64_t)t0 * D + c * 8;
+  // every load issued before any is used: rows past the end re-read the last
+  // row (in bounds) and are zeroed afterwards
   i32x4 raw[NP];
 #pragma unroll
-  for (int p = 0; p < NP; ++p) raw[p] = p * RPI + r < n ? *(const i32x4 *)(base + (int64_t)(p * RPI + r) * D) : i32x4{};
+  for (int p = 0; p < NP; ++p) raw[p] = *(const i32x4 *)(base + (int64_t)min(p * RPI + r, n - 1) * D);
+#pragma unroll
+  for (int p = 0; p < NP; ++p)
+    if (p * RPI + r >= n) raw[p] = i32x4{};
   long long acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0;
@@ -181,7 +186,7 @@ __global__ void k_mean_finalize_kernel(const int64_t *__restrict__ ws, uint16_t 
 //   q = sat_int8(rint(x * (127 / amax))) (amax = 0: scale 0, q 0).
 // Rows in [nvalid, nwrite) are written as zero; every launched block writes
 // its scale (0 for a block without valid rows).
-template <int D>
+template <int D, bool MEAN>
 __device__ __forceinline__ void quant_block(const uint16_t *__restrict__ src, int64_t sts, int64_t shs,
                                             const int32_t *__restrict__ rows, int32_t row0,
                                             const uint16_t *__restrict__ mean, int32_t nvalid, int32_t nwrite,
@@ -193,29 +198,39 @@ __device__ __forceinline__ void quant_block(const uint16_t *__restrict__ src, in
   __shared__ float red[4];
   const int tid = threadIdx.x;
   const int ch = tid % CPR, r0 = tid / CPR;
+  // All loads are issued before any is used (one memory round trip): the
+  // mean as one 16-byte read, rows past nvalid re-read row nvalid - 1 (in
+  // bounds; nvalid >= 1 for every launched block) and are zeroed afterwards.
+  i32x4 mraw = {0, 0, 0, 0};
+  if constexpr (MEAN) mraw = *(const i32x4 *)(mean + h * D + ch * 8);
+  int rix[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int ic = min(blk * TMHD_QUANT_BLOCK + p * RPI + r0, nvalid - 1);
+    rix[p] = rows ? rows[ic] : row0 + ic;
+  }
+  i32x4 raw[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) raw[p] = *(const i32x4 *)(src + (int64_t)rix[p] * sts + (int64_t)h * shs + ch * 8);
   float mf[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) mf[e] = mean ? bf16_bits_to_f32(mean[h * D + ch * 8 + e]) : 0.0f;
+  for (int e = 0; e < 4; ++e) {
+    mf[2 * e] = bf16_bits_to_f32((uint32_t)mraw[e] & 0xffffu);
+    mf[2 * e + 1] = bf16_bits_to_f32((uint32_t)mraw[e] >> 16);
+  }
   float x[NP][8];
   float amax = 0.0f;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    const int i = blk * TMHD_QUANT_BLOCK + p * RPI + r0;
-    if (i < nvalid) {
-      const int row = rows ? rows[i] : row0 + i;
-      const i32x4 raw = *(const i32x4 *)(src + (int64_t)row * sts + (int64_t)h * shs + ch * 8);
+    const bool valid = blk * TMHD_QUANT_BLOCK + p * RPI + r0 < nvalid;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = (uint32_t)raw[e];
-        x[p][2 * e] = bf16_bits_to_f32(w & 0xffffu) - mf[2 * e];
-        x[p][2 * e + 1] = bf16_bits_to_f32(w >> 16) - mf[2 * e + 1];
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[p][e]));
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[p][e] = 0.0f;
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t w = (uint32_t)raw[p][e];
+      x[p][2 * e] = valid ? bf16_bits_to_f32(w & 0xffffu) - mf[2 * e] : 0.0f;
+      x[p][2 * e + 1] = valid ? bf16_bits_to_f32(w >> 16) - mf[2 * e + 1] : 0.0f;
     }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(x[p][e]));
   }
   amax = wave_max(amax);
   if ((tid & 63) == 0) red[tid >> 6] = amax;
@@ -244,7 +259,11 @@ __global__ void __launch_bounds__(256) block_quant_kernel(const uint16_t *__rest
                                                           const uint16_t *__restrict__ mean, int32_t nvalid,
                                                           int32_t nwrite, int8_t *__restrict__ q8, int64_t q8hs,
                                                           float *__restrict__ qscale, int32_t qshs) {
-  quant_block<D>(src, sts, shs, rows, row0, mean, nvalid, nwrite, q8, q8hs, qscale, qshs, blockIdx.y, blockIdx.x);
+  if (mean)
+    quant_block<D, true>(src, sts, shs, rows, row0, mean, nvalid, nwrite, q8, q8hs, qscale, qshs, blockIdx.y, blockIdx.x);
+  else
+    quant_block<D, false>(src, sts, shs, rows, row0, mean, nvalid, nwrite, q8, q8hs, qscale, qshs, blockIdx.y,
+                          blockIdx.x);
 }
 
 // Every key segment's blocks in one launch (slot rows: token stride D); rows up
@@ -253,8 +272,8 @@ template <int D>
 __global__ void __launch_bounds__(256) key_block_quant_kernel(const KeySegs a, const uint16_t *__restrict__ mean) {
   const int sg = key_seg(a, blockIdx.x);
   const int nwrite = (a.tokens[sg] + kTile - 1) / kTile * kTile;
-  quant_block<D>(a.k[sg], D, a.khs[sg], nullptr, 0, mean, a.tokens[sg], nwrite, a.q8[sg], a.q8hs[sg], a.qs[sg],
-                 a.qshs[sg], blockIdx.y, blockIdx.x - a.blk0[sg]);
+  quant_block<D, true>(a.k[sg], D, a.khs[sg], nullptr, 0, mean, a.tokens[sg], nwrite, a.q8[sg], a.q8hs[sg], a.qs[sg],
+                       a.qshs[sg], blockIdx.y, blockIdx.x - a.blk0[sg]);
 }
 
 bool aligned(const void *p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
@@ -371,6 +390,8 @@ extern "C" int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_qu
     return set_error(TMHD_ERR_INVALID, "smooth_quant: bad segment count / heads / lq");
   if (!quant->k_mean || !quant->mean_workspace || !quant->q_i8 || !quant->q_scale)
     return set_error(TMHD_ERR_INVALID, "smooth_quant: null output buffers");
+  if (!aligned(quant->k_mean, 16) || !aligned(quant->mean_workspace, 8))
+    return set_error(TMHD_ERR_INVALID, "smooth_quant: k_mean must be 16-byte and mean_workspace 8-byte aligned");
   const int qcap = (args->lq + 255) / 256 * 256;
   if (quant->q_head_stride < (int64_t)qcap * D || quant->q_scale_head_stride < qcap / TMHD_QUANT_BLOCK ||
       !aligned(quant->q_i8, 16) || quant->q_head_stride % 16)
