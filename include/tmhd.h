@@ -104,6 +104,10 @@ typedef struct tmhd_qk_quant {
   int32_t k_scale_head_stride[TMHD_MAX_SEGMENTS]; /* elements */
   uint16_t *k_mean;             /* bf16 [H][D] written by tmhd_qk_smooth_quant (16-byte aligned) */
   int64_t *mean_workspace;      /* int64 [H][D] scratch (8-byte aligned) */
+  /* Optional, per segment: the exact fixed-point key sums of segment i from
+   * tmhd_k_fixed_sum (int64 [H][D], 8-byte aligned), used in place of summing
+   * its keys again; NULL: summed here.  The mean is the same bits either way. */
+  const int64_t *k_sum[TMHD_MAX_SEGMENTS];
 } tmhd_qk_quant;
 
 /* Library identification: "tmhd <version> gfx950". */
@@ -147,6 +151,17 @@ int tmhd_attn_fwd_i8qk(const tmhd_attn_args *args, const tmhd_qk_quant *quant,
  */
 int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_quant *quant,
                          void *stream);
+
+/*
+ * sum[h][d] = the exact fixed-point sum (rint(k * 2^24) as int64, wrapping)
+ * over the `tokens` slot rows of head h, the per-segment term of the smooth-K
+ * mean: a caller that keeps it for a segment whose keys do not change (a
+ * cached block) passes it in tmhd_qk_quant.k_sum instead of having every call
+ * sum those keys again.  No counterpart in the reference, which recomputes
+ * k.mean over every key per call (src/taomate_hd/inference/sage_value_padding.py:89-92).
+ */
+int tmhd_k_fixed_sum(const void *k, int64_t k_head_stride, int32_t tokens, int32_t heads,
+                     int32_t head_dim, int64_t *sum, void *stream);
 
 /*
  * Copy `n` token-major K/V rows into a slot at token offset `dst`, then zero

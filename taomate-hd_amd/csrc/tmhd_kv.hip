@@ -171,6 +171,20 @@ __global__ void __launch_bounds__(256) k_sum_kernel(const KeySegs a, int64_t *__
   }
 }
 
+// ws[i] = sum over the given per-segment key sums (0 when none are given)
+struct SumList {
+  const int64_t *p[kMaxSeg];
+  int32_t n;
+};
+__global__ void init_sum_kernel(int64_t *__restrict__ ws, const SumList l, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    unsigned long long acc = 0;  // wrapping sum: the same as the atomics' (associative modulo 2^64)
+    for (int s = 0; s < l.n; ++s) acc += (unsigned long long)l.p[s][i];
+    ws[i] = (int64_t)acc;
+  }
+}
+
 __global__ void k_mean_finalize_kernel(const int64_t *__restrict__ ws, uint16_t *__restrict__ mean, int n,
                                        double count) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -296,7 +310,8 @@ int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s
   for (int i = 0; i < a->n_segments; ++i) total += a->seg[i].tokens;
   // 1. exact key sums, 2. bf16 mean
   // one segment table for the key passes; workgroup ranges per pass
-  KeySegs ks{};
+  KeySegs ks{}, sums{};
+  SumList given{};
   ks.n = a->n_segments;
   for (int i = 0; i < a->n_segments; ++i) {
     const tmhd_kv_segment &sg = a->seg[i];
@@ -307,20 +322,26 @@ int smooth_quant(const tmhd_attn_args *a, const tmhd_qk_quant *qq, hipStream_t s
     ks.qs[i] = qq->k_scale[i];
     ks.qshs[i] = qq->k_scale_head_stride[i];
     ks.tokens[i] = sg.tokens;
+    if (qq->k_sum[i]) {  // exact sums given by the caller (tmhd_k_fixed_sum)
+      given.p[given.n++] = qq->k_sum[i];
+    } else {
+      sums.k[sums.n] = ks.k[i];
+      sums.khs[sums.n] = ks.khs[i];
+      sums.tokens[sums.n++] = sg.tokens;
+    }
   }
-  auto ranges = [&](int per) {
-    ks.blk0[0] = 0;
-    for (int i = 0; i < ks.n; ++i) ks.blk0[i + 1] = ks.blk0[i] + (ks.tokens[i] + per - 1) / per;
-    return ks.blk0[ks.n];
+  auto ranges = [](KeySegs &t, int per) {
+    t.blk0[0] = 0;
+    for (int i = 0; i < t.n; ++i) t.blk0[i + 1] = t.blk0[i] + (t.tokens[i] + per - 1) / per;
+    return t.blk0[t.n];
   };
-  hipLaunchKernelGGL(zero_i64_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, H * D);
-  const int nsum = ranges(256);
-  hipLaunchKernelGGL(k_sum_kernel<D>, dim3(nsum, H), dim3(256), 0, s, ks, qq->mean_workspace);
+  hipLaunchKernelGGL(init_sum_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace, given, H * D);
+  if (sums.n) hipLaunchKernelGGL(k_sum_kernel<D>, dim3(ranges(sums, 256), H), dim3(256), 0, s, sums, qq->mean_workspace);
   hipLaunchKernelGGL(k_mean_finalize_kernel, dim3((H * D + 255) / 256), dim3(256), 0, s, qq->mean_workspace,
                      qq->k_mean, H * D, (double)total);
   if (int st = check_launch("smooth-K mean")) return st;
   // 3. keys, every segment in one launch (rows up to the 64-token tile padding are written)
-  const int nblk = ranges(TMHD_QUANT_BLOCK);
+  const int nblk = ranges(ks, TMHD_QUANT_BLOCK);
   hipLaunchKernelGGL(key_block_quant_kernel<D>, dim3(nblk, H), dim3(256), 0, s, ks, (const uint16_t *)qq->k_mean);
   if (int st = check_launch("block_quant keys")) return st;
   // 4. queries (rows up to the 256-row workgroup padding are written)
@@ -400,6 +421,8 @@ extern "C" int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_qu
     return set_error(TMHD_ERR_INVALID, "smooth_quant: query pointer/strides must be 16-byte aligned");
   for (int i = 0; i < args->n_segments; ++i) {
     const tmhd_kv_segment &sg = args->seg[i];
+    if (quant->k_sum[i] && !aligned(quant->k_sum[i], 8))
+      return set_error(TMHD_ERR_INVALID, "smooth_quant: segment %d key sums must be 8-byte aligned", i);
     const int64_t cap = ((int64_t)sg.tokens + kTile - 1) / kTile * kTile;
     if (sg.tokens <= 0 || !sg.k || !aligned(sg.k, 16) || sg.k_head_stride < cap * D || sg.k_head_stride % 8)
       return set_error(TMHD_ERR_INVALID, "smooth_quant: segment %d keys are not a slot", i);
@@ -410,4 +433,29 @@ extern "C" int tmhd_qk_smooth_quant(const tmhd_attn_args *args, const tmhd_qk_qu
   }
   hipStream_t s = (hipStream_t)stream;
   return D == 128 ? smooth_quant<128>(args, quant, s) : smooth_quant<64>(args, quant, s);
+}
+
+extern "C" int tmhd_k_fixed_sum(const void *k, int64_t k_head_stride, int32_t tokens, int32_t heads, int32_t head_dim,
+                                int64_t *sum, void *stream) {
+  using namespace tmhd;
+  if (head_dim != 64 && head_dim != 128) return set_error(TMHD_ERR_UNSUPPORTED, "k_fixed_sum: head_dim %d", head_dim);
+  if (tokens <= 0 || heads <= 0 || k_head_stride < (int64_t)tokens * head_dim || k_head_stride % 8)
+    return set_error(TMHD_ERR_INVALID, "k_fixed_sum: tokens %d heads %d head stride %lld", tokens, heads,
+                     (long long)k_head_stride);
+  if (!k || !sum || !aligned(k, 16) || !aligned(sum, 8))
+    return set_error(TMHD_ERR_INVALID, "k_fixed_sum: keys must be 16-byte and sums 8-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  KeySegs t{};
+  t.n = 1;
+  t.k[0] = (const uint16_t *)k;
+  t.khs[0] = k_head_stride;
+  t.tokens[0] = tokens;
+  t.blk0[0] = 0;
+  t.blk0[1] = (tokens + 255) / 256;
+  hipLaunchKernelGGL(zero_i64_kernel, dim3((heads * head_dim + 255) / 256), dim3(256), 0, s, sum, heads * head_dim);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(k_sum_kernel<128>, dim3(t.blk0[1], heads), dim3(256), 0, s, t, sum);
+  else
+    hipLaunchKernelGGL(k_sum_kernel<64>, dim3(t.blk0[1], heads), dim3(256), 0, s, t, sum);
+  return check_launch("tmhd_k_fixed_sum");
 }

@@ -71,6 +71,7 @@ class QKQuant(ctypes.Structure):
         ("k_scale_head_stride", c_int32 * MAX_SEGMENTS),
         ("k_mean", c_void_p),
         ("mean_workspace", c_void_p),
+        ("k_sum", c_void_p * MAX_SEGMENTS),
     ]
 
 
@@ -139,6 +140,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             c_int32, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_int32, c_int32, c_void_p,
         ],
     ),
+    "tmhd_k_fixed_sum": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "tmhd_token_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_void_p]),
     "tmhd_weight_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),
     "tmhd_gemm_w8a8": (

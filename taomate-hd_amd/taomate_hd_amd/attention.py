@@ -120,6 +120,23 @@ def _row_list(torch: Any, rows: Any, device: Any, limit: int, name: str, checked
     return rows
 
 
+def _key_sum(torch: Any, lib: Any, view: SlotView, stream: int) -> int:
+    """Device address of the exact fixed-point key sums of a slot view (the
+    smooth-K mean's term for that segment), memoised on the slot per (row0,
+    tokens, stream): a cached block's keys are summed once, not on every call.
+    The slot drops the memo whenever it is written."""
+    slot = view.slot
+    key = (int(view.row0), int(view.tokens), int(stream))
+    hit = slot.key_sums.get(key)
+    if hit is None:
+        seg = view.to_segment()
+        hit = torch.empty((slot.heads, slot.head_dim), dtype=torch.int64, device=slot.device)
+        _native.check(lib.tmhd_k_fixed_sum(seg.k, seg.k_head_stride, seg.tokens, slot.heads, slot.head_dim,
+                                           _native.ptr(hit), stream), "tmhd_k_fixed_sum")
+        slot.key_sums[key] = hit
+    return _native.ptr(hit)
+
+
 def segment_attention(
     torch: Any,
     query: Any,
@@ -222,6 +239,8 @@ def segment_attention(
         heads=heads, head_dim=head_dim, lq=lq, tokens=[s.tokens for s in segments], device=query.device
     )
     with maybe_region(timer, "qk_quant"):
+        for i, seg in enumerate(segments):
+            qq.k_sum[i] = _key_sum(torch, lib, seg, stream)
         status = lib.tmhd_qk_smooth_quant(args, qq, stream)
     _native.check(status, "tmhd_qk_smooth_quant")
     with maybe_region(timer, "attention"):

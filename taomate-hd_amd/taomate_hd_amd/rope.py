@@ -90,6 +90,7 @@ def fused_qkv_qk_norm_rope_stage_(qkv: Any, q_weight: Any, k_weight: Any, cos_si
     dst = int(dst)
     if dst < 0 or dst % KV_TILE or dst + n > slot.capacity:
         raise ValueError(f"{n} rows at slot row {dst} do not fit the slot capacity {slot.capacity} (tile-aligned)")
+    slot.key_sums.clear()
     status = _native.load().tmhd_qkv_norm_rope_stage(
         _native.ptr(qkv), tokens, heads, head_dim, qkv.stride(0), _native.ptr(q_weight), _native.ptr(k_weight),
         _native.ptr(cache), cache.stride(0), int(cache.shape[0]), rotary_dim, _native.ptr(positions), float(eps),

@@ -9,7 +9,9 @@ A slot holds one block of keys and values for one layer:
 
 ``cap`` is a multiple of 64 (the kernels' key tile) and rows ``[tokens,
 round_up(tokens, 64))`` are kept zero, so a tile never reads stale data.
-Slots are filled only by ``tmhd_kv_pack``; attention reads them in place.
+Slots are filled only by ``tmhd_kv_pack`` (``KVSlot.pack``) and the staged
+norm + RoPE, which also drop the slot's memo of key sums (``key_sums``, kept
+for the INT8-QK smooth-K mean); attention reads them in place.
 """
 
 from __future__ import annotations
@@ -72,6 +74,9 @@ class KVSlot:
         self.k = torch.empty((self.heads, self.capacity, self.head_dim), dtype=torch.bfloat16, device=self.device)
         self.vt = torch.empty((self.heads, self.head_dim, self.capacity), dtype=torch.bfloat16, device=self.device)
         self.tokens = 0
+        # exact fixed-point key sums of views of this slot, (row0, tokens, stream) ->
+        # int64 [H, D]; dropped whenever the slot is written (pack, staged norm + RoPE)
+        self.key_sums: dict[tuple[int, int, int], Any] = {}
 
     @property
     def nbytes(self) -> int:
@@ -116,6 +121,7 @@ class KVSlot:
         dst = int(dst)
         if dst < 0 or dst % KV_TILE or dst + n > self.capacity:
             raise ValueError(f"{n} rows at slot row {dst} do not fit the slot capacity {self.capacity} (tile-aligned)")
+        self.key_sums.clear()
         lib = _native.load()
         status = lib.tmhd_kv_pack(
             _native.ptr(key), _native.ptr(value), key.stride(0), key.stride(1), rows_ptr, int(row0), n,

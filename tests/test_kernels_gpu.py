@@ -371,3 +371,38 @@ def test_row_lists_checked_before_any_launch(torch_mod, dev):
                             out=out, o_rows=torch.tensor([4, 0], dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
     assert res is out and bool(torch.isfinite(out).all())
+
+
+def test_i8qk_key_sum_memo_hits_and_invalidation(torch_mod, dev):
+    """The smooth-K key sums memoised per slot view give the same quantised
+    operands and output as summing afresh; re-packing a slot drops its memo,
+    so the next call sees the new keys (compared with a fresh slot)."""
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    heads, dim, lq, splits = 3, 128, 300, [400, 333]
+    q = to_dev(randn_bf16((lq, heads, dim), 60), dev)
+    k = randn_bf16((sum(splits), heads, dim), 61, offset=key_offset(heads, dim, 62))
+    v = randn_bf16((sum(splits), heads, dim), 63)
+    views = _slots(torch, dev, k, v, splits)
+
+    def run(vs):
+        out, qv = segment_attention(torch, q, vs, scale=dim ** -0.5, backend="i8qk", return_quant=True)
+        torch.cuda.synchronize()
+        return out.clone(), qv["k_mean"].clone(), [t.clone() for t in qv["k_i8"]]
+
+    first = run(views)
+    assert all(len(vw.slot.key_sums) == 1 for vw in views)
+    second = run(views)  # memo hits
+    assert torch.equal(first[0].view(torch.int16), second[0].view(torch.int16))
+    assert torch.equal(first[1].view(torch.int16), second[1].view(torch.int16))
+    assert all(torch.equal(a, b) for a, b in zip(first[2], second[2]))
+    # new keys in the second slot: its memo is dropped by the pack
+    k2 = randn_bf16((splits[1], heads, dim), 64, offset=key_offset(heads, dim, 65))
+    views[1].slot.pack(to_dev(k2, dev), to_dev(v[splits[0]:], dev))
+    assert not views[1].slot.key_sums
+    third = run(views)
+    fresh = run(_slots(torch, dev, np.concatenate([k[: splits[0]], k2]), v, splits))
+    assert torch.equal(third[1].view(torch.int16), fresh[1].view(torch.int16))
+    assert not torch.equal(third[1].view(torch.int16), first[1].view(torch.int16))
+    assert torch.equal(third[0].view(torch.int16), fresh[0].view(torch.int16))
