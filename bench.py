@@ -497,6 +497,9 @@ def main() -> int:
             "frac_mixed_peak": round(tflops / (PEAK_BF16_TFLOPS * 4.0 / 3.0), 4),
             "kernel_tflops": round(ATTN_FLOPS / (attn_ms * 1e-3) / 1e12, 2),
             "components_ms": {k: round(v["mean_ms"], 4) for k, v in comps.items()},
+            "note": "qk_quant sums the chunk's own keys each call; the cached blocks' exact key sums are kept "
+                    "on their slots from the first (warm-up) call, as in streaming, where a committed block's "
+                    "keys do not change between calls",
         }
         if result["value"]:
             entry["speedup_vs_bf16"] = round(tflops / result["value"], 3)
