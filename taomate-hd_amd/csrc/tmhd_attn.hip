@@ -538,7 +538,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // load n of a tile: K blocks first (n < KWL), then V blocks
   constexpr int NLD = KWL + VWL;
   static_assert(NLD <= 16, "slot plan bounds");
-  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, 3 * NS / 2, I8);  // sub-tiles with tile loads
+  // tile loads spread over the first 1.5 NS regions (BF16) or all of them (INT8: 1.3% faster in a
+  // same-box A/B, BF16 unchanged)
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : 3 * NS / 2, I8);  // sub-tiles with tile loads
   constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8);               // sub-tiles without
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
