@@ -380,7 +380,9 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 //   C(u): their bf16 pack and row-sum adds (4 each), at or after E(u) and at
 //         least one MFMA before the P.V MFMA that reads the pack;
 //   M(u): INT8 dequantisation and row maximum of pair u % 8, half u / 8 of
-//         the next sub-tile's scores, after the score-read guard;
+//         the next sub-tile's scores, after the score-read guard (costed 4
+//         for BF16, 8 for INT8: below its 12 issue cycles, which spreads the
+//         INT8 units more evenly and measured 1.5-2% faster than 12);
 //   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions.
 // Every region starts with its share of the fixed work (the operand read of
 // odd regions, the wait in front of each slot's first MFMA); each unit goes
@@ -412,7 +414,7 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
       s.c[u] = plan_put(cost, s.e[u], dl, 12);
     }
   for (int q = 0; q < 8; ++q)
-    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 12 : 4);
+    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
   for (int q = 4; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
