@@ -220,8 +220,17 @@ class HookOracle:
             return out
         return attention.attention_fp64(q, np.concatenate(ks), np.concatenate(vs), scale)
 
-    def __call__(self, layer, q, k, v, token_tags, commit_mask, boundaries, scale, live_documents_hint=None):
-        """q/k/v float32 [T, H, D] (bf16 values), commit_mask bool [T]."""
+    def __call__(self, layer, q, k, v, token_tags, commit_mask, boundaries, scale, live_documents_hint=None,
+                 cached_documents=(), compact_rows=None):
+        """q/k/v float32 [T, H, D] (bf16 values), commit_mask bool [T].
+
+        ``cached_documents``: live documents whose condition attention the
+        condition cache reuses (condition_cache.py:322-329): their condition
+        query rows are not computed and read zero (attention_hook.py:445-450),
+        while media queries still attend over their condition keys.
+        ``compact_rows``: the sorted rows the condition cache keeps in its
+        compact order (condition_cache.py:173-228); the output then holds only
+        those rows, in that order (rows nobody writes stay zero)."""
         if self.mode == "idle":
             raise RuntimeError("patched H3 attention called outside a streaming step")
         bounds = tuple(int(b) for b in boundaries)
@@ -271,7 +280,7 @@ class HookOracle:
                 media_parts.append(previous)
             media_parts.append((ks[media], vs[media]))
             media_parts = [p for p in media_parts if p[0].shape[0] > 0]
-            if len(cond):
+            if len(cond) and index not in cached_documents:
                 out[start + cond] = self._exact(qs[cond], [cond_kv], scale)
             if len(media):
                 out[start + media] = self._exact(qs[media], media_parts, scale)
@@ -279,6 +288,8 @@ class HookOracle:
             self.cache.stage(layer, k, v, token_tags, commit_mask)
         elif fused:
             self.cache.stage(layer, k, v, token_tags, commit_mask, commit_indices=prev_media_idx)
+        if compact_rows is not None:
+            return out[np.asarray(compact_rows, dtype=np.int64)]
         return out
 
 

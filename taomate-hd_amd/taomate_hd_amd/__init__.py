@@ -11,7 +11,7 @@ non-streamed forwards (model/layers.py ``_packed_sdpa``).  All compute runs in
 the hand-written HIP kernels of libtmhd.so; nothing falls back to the CPU.
 """
 
-from . import _native
+from . import _native, condition
 from .attention import QKQuantWorkspace, segment_attention
 from .capability import (
     STREAM_HOOK_ABI,

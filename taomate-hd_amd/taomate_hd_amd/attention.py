@@ -24,12 +24,20 @@ class QKQuantWorkspace:
     """Grow-only INT8-QK operand storage, keyed by (device, stream).
 
     Work on one stream is ordered, so a call may reuse the buffers of the
-    previous call on that stream without synchronising.
+    previous call on that stream without synchronising.  ``nbytes`` reports
+    what it holds and ``release`` returns it to the allocator.
     """
 
     def __init__(self, torch: Any) -> None:
         self._torch = torch
         self._buffers: dict[tuple[Any, ...], dict[str, Any]] = {}
+
+    @property
+    def nbytes(self) -> int:
+        return sum(int(t.numel()) * t.element_size() for store in self._buffers.values() for t in store.values())
+
+    def release(self) -> None:
+        self._buffers.clear()
 
     def _grow(self, store: dict[str, Any], name: str, numel: int, dtype: Any, device: Any) -> Any:
         buf = store.get(name)
@@ -100,6 +108,16 @@ def split_workspace(torch: Any, device: Any, head_dim: int) -> Any:
     return buf
 
 
+def split_workspace_bytes() -> int:
+    """Bytes held by the split workspaces of every (device, stream) so far."""
+    return sum(int(buf.numel()) for buf in _SPLIT_WORKSPACES.values())
+
+
+def release_split_workspaces() -> None:
+    """Return the split workspaces to the allocator (the next call regrows its own)."""
+    _SPLIT_WORKSPACES.clear()
+
+
 def _validate_tokens_major(torch: Any, tensor: Any, name: str) -> None:
     _native.require_device_tensor(torch, tensor, name)
     if tensor.dtype != torch.bfloat16 or tensor.ndim != 3 or tensor.stride(2) != 1:
@@ -112,12 +130,15 @@ def _row_list(torch: Any, rows: Any, device: Any, limit: int, name: str, checked
     callers whose lists are valid by construction pass ``checked``."""
     if not torch.is_tensor(rows) or rows.device != torch.device(device):
         raise ValueError(f"{name} must be a tensor on the GPU of the rows it indexes")
-    rows = rows.reshape(-1).to(torch.int32).contiguous()
+    if rows.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"{name} must be an int32 or int64 tensor")
+    rows = rows.reshape(-1)
     if not checked and rows.numel():
+        # on the list as given: an int64 entry past 2^31 must not wrap into range
         lo, hi = (int(v) for v in torch.aminmax(rows))
         if lo < 0 or hi >= limit:
             raise ValueError(f"{name} entries must lie in [0, {limit})")
-    return rows
+    return rows.to(torch.int32).contiguous()
 
 
 def _key_sum(torch: Any, lib: Any, view: SlotView, stream: int) -> int:

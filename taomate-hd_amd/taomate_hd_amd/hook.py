@@ -29,7 +29,7 @@ from __future__ import annotations
 from enum import Enum
 from typing import Any, Callable
 
-from . import _native
+from . import _native, condition
 from .attention import QKQuantWorkspace, segment_attention
 from .kvcache import HeadMajorRingKVCache
 from .profiling import ComponentTimer, maybe_region
@@ -132,6 +132,12 @@ class StreamingAttentionHook:
         self._fused_previous_media_indices: Any | None = None
         self._live_document_rows: dict[int, tuple[_Rows, _Rows]] = {}
         self._staged_match: dict[int, bool] = {}
+        # the condition-cache queries (attention_hook.py:322-324, 445-465): the
+        # runtime's own unless injected (condition.resolve)
+        if condition_attention_cached is None or compact_condition_attention_output is None:
+            resolved_cached, resolved_compact = condition.resolve()
+            condition_attention_cached = condition_attention_cached or resolved_cached
+            compact_condition_attention_output = compact_condition_attention_output or resolved_compact
         self._condition_attention_cached = condition_attention_cached
         self._compact_output = compact_condition_attention_output
         self._scratch: SlotPool | None = None
@@ -393,7 +399,7 @@ class StreamingAttentionHook:
                 )
         staged_view = self.cache.staged_view(layer_name)
 
-        compact = None if self._compact_output is None else self._compact_output(layer_name, query)
+        compact = self._compact_output(layer_name, query)
         out = torch.empty_like(query) if compact is None else None
         try:
             history = self.cache.history_views(layer_name)
@@ -432,10 +438,7 @@ class StreamingAttentionHook:
                     previous_view = staged_view
                 else:
                     prefixes = list(history)
-                cached = bool(
-                    self._condition_attention_cached is not None
-                    and self._condition_attention_cached(layer_name, index)
-                )
+                cached = bool(self._condition_attention_cached(layer_name, index))
                 if condition_rows.count:
                     if cached:
                         if out is not None:

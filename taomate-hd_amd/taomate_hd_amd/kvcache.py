@@ -304,8 +304,11 @@ class HeadMajorRingKVCache:
         import torch
 
         if self._pool is None:
+            # evicting a block frees one slot per layer, which the next stage takes
+            # back: keep up to two blocks' worth free
             self._pool = SlotPool(
-                torch, heads=self.contract.local_heads, head_dim=self.contract.head_dim, device=device
+                torch, heads=self.contract.local_heads, head_dim=self.contract.head_dim, device=device,
+                max_free=2 * len(self.contract.layer_names),
             )
             self._device = torch.device(device)
         elif torch.device(device) != self._device:

@@ -146,14 +146,27 @@ class KVSlot:
 
 
 class SlotPool:
-    """Grow-only pool of slots of one shape family, recycled without copies."""
+    """Pool of slots of one shape family, recycled without copies.
 
-    def __init__(self, torch: Any, *, heads: int, head_dim: int, device: Any) -> None:
+    ``acquire`` hands out the smallest free slot that fits (or a new one);
+    ``release`` takes it back.  At most ``max_free`` slots are kept free:
+    beyond that the smallest free slot is returned to the allocator, so a
+    pool's idle memory stays bounded (``free_bytes``).
+    """
+
+    def __init__(self, torch: Any, *, heads: int, head_dim: int, device: Any, max_free: int = 8) -> None:
+        if int(max_free) < 0:
+            raise ValueError("max_free must be non-negative")
         self._torch = torch
         self.heads = heads
         self.head_dim = head_dim
         self.device = device
+        self.max_free = int(max_free)
         self._free: list[KVSlot] = []
+
+    @property
+    def free_bytes(self) -> int:
+        return sum(slot.nbytes for slot in self._free)
 
     def acquire(self, tokens: int) -> KVSlot:
         need = round_up(max(int(tokens), 1), KV_TILE)
@@ -170,6 +183,8 @@ class SlotPool:
     def release(self, slot: KVSlot) -> None:
         slot.tokens = 0
         self._free.append(slot)
+        if len(self._free) > self.max_free:
+            self._free.remove(min(self._free, key=lambda s: s.capacity))
 
     def clear(self) -> None:
         self._free.clear()

@@ -1,9 +1,10 @@
 """Selective W8A8 projection: drop-in for src/taomate_hd/inference/w8a8.py and
 the ``_linear`` dispatch of src/taomate_hd/distributed/linear.py:43-68.
 
-* ``W8A8Workspace`` mirrors ``CutlassW8A8Workspace`` (w8a8.py:12-73): grow-only
-  activation / scale / output buffers per (device, stream, width), then
-  ``dynamic_scaled_int8_quant`` + ``cutlass_scaled_mm`` into them.
+* ``W8A8Workspace`` plays the role of ``CutlassW8A8Workspace`` (w8a8.py:12-73):
+  per-stream storage for the quantized activations (one arena) and the bf16
+  outputs (one buffer per output width), then ``dynamic_scaled_int8_quant`` +
+  ``cutlass_scaled_mm`` into them.
 * ``cutlass_w8a8_linear`` (w8a8.py:117-145) also accepts a bf16 bias, applied
   in the GEMM epilogue (the reference raises for a bias).
 * ``resolve_h3_cutlass_w8a8_policy`` restates the interior QKV/FC1 selection
@@ -25,46 +26,90 @@ INTERIOR_FC1_QKV_CUTLASS_W8A8_POLICY = "interior_fc1_qkv_v1"
 H3_CUTLASS_W8A8_POLICIES = (INTERIOR_FC1_QKV_CUTLASS_W8A8_POLICY,)
 
 
+def _stream_of(torch: Any, tensor: Any) -> tuple[str, int | None, int]:
+    """(device type, index, stream handle) of the stream work on ``tensor`` is queued on."""
+    device = tensor.device
+    handle = int(torch.cuda.current_stream(device=device).cuda_stream) if device.type == "cuda" else 0
+    return (device.type, device.index, handle)
+
+
+class _StreamStorage:
+    """Device memory of one stream: a byte arena holding the quantized
+    activations (int8 rows, then their fp32 scales at a 256-byte aligned
+    offset), and one bf16 output buffer per output width."""
+
+    def __init__(self) -> None:
+        self.arena: Any | None = None
+        self.outputs: dict[int, Any] = {}
+
+    def nbytes(self) -> int:
+        total = 0 if self.arena is None else int(self.arena.numel())
+        return total + sum(int(t.numel()) * 2 for t in self.outputs.values())
+
+
 class W8A8Workspace:
-    """Reusable per-stream INT8 activation and bf16 output storage (w8a8.py:12-73)."""
+    """Projection storage reused per stream (the role of the reference's
+    ``CutlassW8A8Workspace``, w8a8.py:12-73).
 
-    def __init__(self, torch: Any) -> None:
+    Work on one stream is ordered, so every call on a stream shares one
+    arena for its quantized activations: the next call's quantization is
+    queued behind the previous call's GEMM.  A call's bf16 output lives in a
+    buffer kept per output width and stays valid until the next call on the
+    same stream with the same output width.  Storage grows to the largest
+    call seen; ``max_bytes`` (optional) bounds the total per workspace,
+    ``nbytes`` reports it and ``release`` returns it to the allocator.
+    """
+
+    def __init__(self, torch: Any, *, max_bytes: int | None = None) -> None:
         self._torch = torch
-        self._activation: dict[tuple[Any, ...], tuple[Any, Any]] = {}
-        self._outputs: dict[tuple[Any, ...], Any] = {}
+        self._max_bytes = None if max_bytes is None else int(max_bytes)
+        self._streams: dict[tuple[Any, ...], _StreamStorage] = {}
 
-    def _stream_key(self, inputs: Any) -> tuple[Any, ...]:
-        device = inputs.device
-        if device.type != "cuda":
-            return (device.type, device.index, 0)
-        stream = self._torch.cuda.current_stream(device=device)
-        return (device.type, device.index, int(stream.cuda_stream))
+    @property
+    def nbytes(self) -> int:
+        return sum(s.nbytes() for s in self._streams.values())
 
-    def _activation_buffers(self, inputs: Any, stream_key: tuple[Any, ...]) -> tuple[Any, Any]:
+    def release(self) -> None:
+        self._streams.clear()
+
+    def _storage(self, inputs: Any) -> _StreamStorage:
+        return self._streams.setdefault(_stream_of(self._torch, inputs), _StreamStorage())
+
+    def _reserve(self, grow_by: int) -> None:
+        if self._max_bytes is not None and self.nbytes + grow_by > self._max_bytes:
+            raise MemoryError(f"W8A8 workspace would exceed its {self._max_bytes}-byte bound")
+
+    def activations(self, inputs: Any) -> tuple[Any, Any]:
+        """int8 ``[rows, width]`` and fp32 ``[rows, 1]`` views for the quantized ``inputs``."""
+        torch = self._torch
         rows, width = int(inputs.shape[0]), int(inputs.shape[1])
-        key = (*stream_key, width)
-        existing = self._activation.get(key)
-        if existing is None or int(existing[0].shape[0]) < rows:
-            existing = (
-                self._torch.empty((rows, width), device=inputs.device, dtype=self._torch.int8),
-                self._torch.empty((rows, 1), device=inputs.device, dtype=self._torch.float32),
-            )
-            self._activation[key] = existing
-        return existing[0][:rows], existing[1][:rows]
+        scale_at = (rows * width + 255) // 256 * 256
+        need = scale_at + 4 * rows
+        store = self._storage(inputs)
+        if store.arena is None or int(store.arena.numel()) < need:
+            self._reserve(need - (0 if store.arena is None else int(store.arena.numel())))
+            store.arena = None  # let the allocator reuse the old block
+            store.arena = torch.empty(need, dtype=torch.uint8, device=inputs.device)
+        quantized = store.arena[: rows * width].view(torch.int8).view(rows, width)
+        scales = store.arena[scale_at:need].view(torch.float32).view(rows, 1)
+        return quantized, scales
 
-    def _output_buffer(self, inputs: Any, output_width: int, stream_key: tuple[Any, ...]) -> Any:
-        rows = int(inputs.shape[0])
-        key = (*stream_key, int(output_width))
-        existing = self._outputs.get(key)
-        if existing is None or int(existing.shape[0]) < rows:
-            existing = self._torch.empty((rows, int(output_width)), device=inputs.device, dtype=self._torch.bfloat16)
-            self._outputs[key] = existing
-        return existing[:rows]
+    def output(self, inputs: Any, width: int) -> Any:
+        """The bf16 ``[rows, width]`` output buffer of a call."""
+        torch = self._torch
+        rows, width = int(inputs.shape[0]), int(width)
+        store = self._storage(inputs)
+        buf = store.outputs.get(width)
+        if buf is None or int(buf.shape[0]) < rows:
+            self._reserve(2 * width * (rows - (0 if buf is None else int(buf.shape[0]))))
+            store.outputs.pop(width, None)
+            buf = torch.empty((rows, width), dtype=torch.bfloat16, device=inputs.device)
+            store.outputs[width] = buf
+        return buf[:rows]
 
     def linear(self, inputs: Any, weight_t: Any, weight_scale: Any, bias: Any | None = None) -> Any:
-        stream_key = self._stream_key(inputs)
-        quantized, activation_scale = self._activation_buffers(inputs, stream_key)
-        output = self._output_buffer(inputs, int(weight_t.shape[1]), stream_key)
+        quantized, activation_scale = self.activations(inputs)
+        output = self.output(inputs, int(weight_t.shape[1]))
         quant.dynamic_scaled_int8_quant(quantized, inputs, activation_scale, None)
         quant.cutlass_scaled_mm_out(output, quantized, weight_t, activation_scale, weight_scale, bias)
         return output
@@ -156,7 +201,7 @@ def cutlass_w8a8_linear_swiglu(torch: Any, inputs: Any, weight: Any, weight_scal
     shape = (*inputs.shape[:-1], int(weight.shape[0]) // 2)
     flattened = inputs.reshape(-1, int(inputs.shape[-1])).contiguous()
     if workspace is not None:
-        quantized, activation_scale = workspace._activation_buffers(flattened, workspace._stream_key(flattened))
+        quantized, activation_scale = workspace.activations(flattened)
         quant.dynamic_scaled_int8_quant(quantized, flattened, activation_scale, None)
     else:
         quantized, activation_scale, _ = quant.scaled_int8_quant(flattened)

@@ -109,15 +109,21 @@ def test_stream_noisy_commit_retain_sequence(torch_mod, dev, backend):
         assert receipt["kernel_calls"] > 0 and receipt["smooth_k"]
 
 
-def test_stream_fused_progress_denoise(torch_mod, dev):
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_stream_fused_progress_denoise(torch_mod, dev, backend):
+    """Fused progress-denoise steps (staged previous media, recent / sink
+    prefix views, the video-only shortened sink) against the oracle; the
+    INT8-QK backend also checks the per-slot key-sum memo on those views."""
     torch = torch_mod
     from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
     from taomate_hd_amd.hook import HookMode
 
     cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
-    hook = StreamingAttentionHook(cache)
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
     ocache = ost.CacheOracle(LAYERS)
-    ohook = ost.HookOracle(ocache)
+    ohook = ost.HookOracle(ocache, backend=backend)
+    exact_cache = ost.CacheOracle(LAYERS)
+    exact_hook = ost.HookOracle(exact_cache)
     tags1, mask1, b1 = ost.packed_layout(9, 0, 6, 40, align=8)
     tags2, mask2, b2 = ost.packed_layout(5, 0, 8, 48, align=8)
     # packed pair: previous document (being committed) + current document
@@ -126,40 +132,44 @@ def test_stream_fused_progress_denoise(torch_mod, dev):
     bounds = (*b1, *(len(tags1) + b for b in b2[1:]))
     seed = 500
 
+    caches = (cache, ocache, exact_cache)
+
     def run(mode, block, layout, hint=None, **kw):
         nonlocal seed
         t_, m_, b_ = layout
         hook.activate(mode=HookMode(mode), block_index=block, **kw)
-        ohook.activate(mode, block, kw.get("fused_current_use_sink"), kw.get("fused_current_recent_blocks"))
+        for o in (ohook, exact_hook):
+            o.activate(mode, block, kw.get("fused_current_use_sink"), kw.get("fused_current_recent_blocks"))
         for layer in LAYERS:
             q, k, v = _qkv(len(t_), seed)
             seed += 10
             got, want = _call(torch, dev, hook, ohook, layer, q, k, v, t_, m_, b_, hint=hint)
-            _check("sdpa", got, want)
+            exact = exact_hook(layer, q, k, v, t_, m_, b_, D ** -0.5, live_documents_hint=hint)
+            _check(backend, got, want, exact)
         hook.deactivate()
         ohook.deactivate()
+        exact_hook.deactivate()
 
     for block in range(4):
         # fused variants against the current cache depth (rolled back)
         for recent, sink in ((2, True), (3, True), (1, True), (2, False), (None, None)):
             kw = {} if recent is None else {"fused_current_use_sink": sink, "fused_current_recent_blocks": recent}
-            cache.begin_clean_commit(block)
-            ocache.begin_clean_commit(block)
+            for c in caches:
+                c.begin_clean_commit(block)
             run("fused_progress_denoise", block, (tags, mask, bounds), hint=(0, 2), **kw)
-            cache.rollback()
-            ocache.rollback()
+            for c in caches:
+                c.rollback()
         # then commit this block through a fused step (or a plain clean commit)
-        cache.begin_clean_commit(block)
-        ocache.begin_clean_commit(block)
+        for c in caches:
+            c.begin_clean_commit(block)
         if block % 2:
             run("fused_progress_denoise", block, (tags, mask, bounds), fused_current_use_sink=True,
                 fused_current_recent_blocks=2)
         else:
             run("clean_commit", block, (tags1, mask1, b1))
-        cache.commit()
-        ocache.commit()
-        cache.retain_sink_and_recent_commits(2)
-        ocache.retain_sink_and_recent_commits(2)
+        for c in caches:
+            c.commit()
+            c.retain_sink_and_recent_commits(2)
         assert list(cache.commit_token_tags) == ocache.tags
         for layer in LAYERS:
             pair = cache.history(layer)
@@ -173,15 +183,18 @@ def test_stream_fused_progress_denoise(torch_mod, dev):
                 assert np.array_equal(bf16.from_torch(fk.value), ov)
 
 
-def test_noncontiguous_commit_mask_and_empty_documents(torch_mod, dev):
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_noncontiguous_commit_mask_and_empty_documents(torch_mod, dev, backend):
     torch = torch_mod
     from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
     from taomate_hd_amd.hook import HookMode
 
     cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS[:1], local_heads=H, head_dim=D))
-    hook = StreamingAttentionHook(cache)
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
     ocache = ost.CacheOracle(LAYERS[:1])
-    ohook = ost.HookOracle(ocache)
+    ohook = ost.HookOracle(ocache, backend=backend)
+    exact_cache = ost.CacheOracle(LAYERS[:1])
+    exact_hook = ost.HookOracle(exact_cache)
     T = 150
     rng = np.random.default_rng(3)
     mask = np.zeros(T, dtype=bool)
@@ -193,18 +206,21 @@ def test_noncontiguous_commit_mask_and_empty_documents(torch_mod, dev):
     bounds = (0, 0, 140, 140, 150)  # empty documents at both ends of the live one
     for block, mode in ((0, "noisy"), (0, "clean_commit"), (1, "noisy")):
         if mode == "clean_commit":
-            cache.begin_clean_commit(block)
-            ocache.begin_clean_commit(block)
+            for c in (cache, ocache, exact_cache):
+                c.begin_clean_commit(block)
         hook.activate(mode=HookMode(mode), block_index=block)
         ohook.activate(mode, block)
+        exact_hook.activate(mode, block)
         q, k, v = _qkv(T, 900 + block)
         got, want = _call(torch, dev, hook, ohook, LAYERS[0], q, k, v, tags, mask, bounds)
-        _check("sdpa", got, want)
+        exact = exact_hook(LAYERS[0], q, k, v, tags, mask, bounds, D ** -0.5)
+        _check(backend, got, want, exact)
         hook.deactivate()
         ohook.deactivate()
+        exact_hook.deactivate()
         if mode == "clean_commit":
-            cache.commit()
-            ocache.commit()
+            for c in (cache, ocache, exact_cache):
+                c.commit()
     pair = cache.history(LAYERS[0])
     wk, wv = ocache.history(LAYERS[0])
     assert np.array_equal(bf16.from_torch(pair.key), wk)
@@ -298,3 +314,91 @@ def test_prestaged_chunk_used_without_pack(torch_mod, dev, monkeypatch):
     slot = hook._prestaged[LAYERS[0]][0]
     hook.deactivate()
     assert not hook._prestaged and any(f is slot for f in hook._scratch._free)
+
+
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_condition_cache_cached_rows_and_compact_output(torch_mod, dev, backend):
+    """The condition cache as the hook sees it (attention_hook.py:322-324,
+    445-465): a cached document's condition query rows read zero while its
+    media rows still attend over the condition keys; with the compact order
+    the hook returns only the kept rows (media rows through write_rows, the
+    padding document through write_document).  Noisy, clean-commit and
+    noisy-over-history calls through the drop-in session, against the
+    oracle with the same decisions."""
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingSession, condition
+
+    class Plan:
+        phases = ("p0", "p1")
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=LAYERS, local_heads=H, head_dim=D))
+    ocache = ost.CacheOracle(LAYERS)
+    ohook = ost.HookOracle(ocache, backend=backend)
+    exact_cache = ost.CacheOracle(LAYERS)
+    exact_hook = ost.HookOracle(exact_cache)
+    tags, mask, bounds = ost.packed_layout(37, 20, 14, 90)  # doc 0 live (rows 0..160), doc 1 padding
+    T = len(tags)
+    condition_rows = set(range(0, 57))
+    dropped_padding = set(range(170, 176))
+    variants = [
+        ((), None),
+        ((0,), None),
+        ((0,), [r for r in range(T) if r not in condition_rows]),
+        ((0,), [r for r in range(T) if r not in condition_rows | dropped_padding]),
+        ((), [r for r in range(T) if r not in dropped_padding]),
+    ]
+    seed = 700
+
+    def step(block, mode, decisions):
+        nonlocal seed
+        for layer in LAYERS:
+            q, k, v = _qkv(T, seed)
+            seed += 10
+            cached_docs, kept = decisions
+            state = condition.ConditionLayerState(layer, cached_documents=cached_docs, compact_rows=kept, seq_len=T)
+            with condition.condition_layer(state):
+                out = session.hook(
+                    attention=_Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
+                    value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
+                    commit_mask=torch.tensor(mask, device=dev), cu_seqlens=None, cu_seqlens_host=tuple(bounds),
+                    max_seqlen=T)
+            torch.cuda.synchronize()
+            kw = {"cached_documents": cached_docs, "compact_rows": kept}
+            want = ohook(layer, q, k, v, tags, mask, bounds, D ** -0.5, **kw)
+            exact = exact_hook(layer, q, k, v, tags, mask, bounds, D ** -0.5, **kw)
+            got = bf16.from_torch(out)
+            assert got.shape == want.shape
+            if 0 in cached_docs and kept is None:
+                assert np.all(got[sorted(condition_rows)] == 0)
+            _check(backend, got, want, exact)
+
+    with StreamingSession(Plan(), cache=cache, attention_backend=backend) as session:
+        for i, decisions in enumerate(variants):
+            with session.noisy_step(0):
+                ohook.activate("noisy", 0)
+                exact_hook.activate("noisy", 0)
+                step(0, "noisy", decisions)
+                ohook.deactivate()
+                exact_hook.deactivate()
+        with session.clean_commit(0):
+            for c in (ocache, exact_cache):
+                c.begin_clean_commit(0)
+            ohook.activate("clean_commit", 0)
+            exact_hook.activate("clean_commit", 0)
+            step(0, "clean_commit", variants[2])
+            ohook.deactivate()
+            exact_hook.deactivate()
+        for c in (ocache, exact_cache):
+            c.commit()
+        for decisions in variants[1:4]:
+            with session.noisy_step(1):
+                ohook.activate("noisy", 1)
+                exact_hook.activate("noisy", 1)
+                step(1, "noisy", decisions)
+                ohook.deactivate()
+                exact_hook.deactivate()
+    for layer in LAYERS:
+        pair = cache.history(layer)
+        wk, wv = ocache.history(layer)
+        assert np.array_equal(bf16.from_torch(pair.key), wk)
+        assert np.array_equal(bf16.from_torch(pair.value), wv)

@@ -297,3 +297,106 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=300, cwd=str(REPO))
     assert r.returncode == 2
     assert "one GPU only" in r.stderr and r.stdout == ""
+
+
+def test_condition_cache_queries_and_compact_writer_without_gpu():
+    import torch
+
+    from taomate_hd_amd import condition
+
+    cached_fn, compact_fn = condition.resolve()
+    assert cached_fn is condition.condition_attention_cached  # no reference runtime here
+    assert compact_fn is condition.compact_condition_attention_output
+    q = torch.zeros((10, 2, 4), dtype=torch.bfloat16)
+    assert not cached_fn("blocks.0.attn", 0) and compact_fn("blocks.0.attn", q) is None
+    state = condition.ConditionLayerState("blocks.0", cached_documents=(1,))
+    with condition.condition_layer(state):
+        assert cached_fn("blocks.0.attn", 1) and not cached_fn("blocks.0.attn", 0)
+        assert not cached_fn("blocks.1.attn", 1)
+        assert compact_fn("blocks.0.attn", q) is None  # no compact order
+    assert not cached_fn("blocks.0.attn", 1)
+    with pytest.raises(ValueError, match="sorted"):
+        condition.ConditionLayerState("blocks.0", compact_rows=[3, 2])
+    state = condition.ConditionLayerState("blocks.0.attn", cached_documents=(0,), compact_rows=[2, 3, 5, 7, 8, 9])
+    with condition.condition_layer(state):
+        assert compact_fn("blocks.1.attn", q) is None
+        writer = compact_fn("blocks.0.attn", q)
+        assert tuple(writer.output.shape) == (6, 2, 4) and not bool(writer.output.any())
+        value = torch.arange(1, 3, dtype=torch.bfloat16).view(2, 1, 1).expand(2, 2, 4)
+        writer.write_rows(0, "media", 1, torch.tensor([2, 4]), value)  # global rows 3, 5
+        doc = torch.arange(10, 13, dtype=torch.bfloat16).view(3, 1, 1).expand(3, 2, 4)
+        writer.write_document(7, 10, doc)  # global rows 7..9, all kept
+        assert writer.output[:, 0, 0].tolist() == [0, 1, 2, 10, 11, 12]
+        with pytest.raises(ValueError, match="compact row set"):
+            writer.write_rows(0, "condition", 0, torch.tensor([0, 1]), value)  # rows 0, 1 not kept
+
+
+def test_session_forwards_condition_cache_queries_without_gpu():
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingSession, condition
+
+    class Plan:
+        phases = ("p0",)
+
+    def cached(layer, doc):
+        return False
+
+    def compact(layer, query):
+        return None
+
+    cache = HeadMajorRingKVCache(KVContract(layer_names=("blocks.0.attn",), local_heads=2, head_dim=64))
+    session = StreamingSession(Plan(), cache=cache, condition_attention_cached=cached,
+                               compact_condition_attention_output=compact)
+    assert session.hook._condition_attention_cached is cached and session.hook._compact_output is compact
+    default = StreamingSession(Plan(), cache=cache)
+    assert default.hook._condition_attention_cached is condition.condition_attention_cached
+
+
+def test_w8a8_workspace_storage_without_gpu():
+    import torch
+
+    from taomate_hd_amd import W8A8Workspace
+
+    ws = W8A8Workspace(torch, max_bytes=1 << 20)
+    x = torch.zeros((100, 256))
+    q, s = ws.activations(x)
+    assert q.dtype == torch.int8 and tuple(q.shape) == (100, 256)
+    assert s.dtype == torch.float32 and tuple(s.shape) == (100, 1)
+    assert s.data_ptr() % 256 == 0 and s.data_ptr() >= q.data_ptr() + q.numel()
+    q2, _ = ws.activations(torch.zeros((10, 512)))  # smaller: same arena
+    assert q2.data_ptr() == q.data_ptr()
+    a = ws.output(x, 384)
+    b = ws.output(x, 128)
+    assert a.dtype == torch.bfloat16 and tuple(a.shape) == (100, 384) and a.data_ptr() != b.data_ptr()
+    assert ws.output(x[:7], 384).data_ptr() == a.data_ptr()  # same width: reused
+    assert ws.nbytes == (100 * 256 + 4 * 100) + 2 * 100 * (384 + 128)
+    with pytest.raises(MemoryError, match="bound"):
+        ws.output(torch.zeros((4096, 1)), 4096)
+    ws.release()
+    assert ws.nbytes == 0
+
+
+def test_slot_pool_keeps_at_most_max_free_slots_without_gpu():
+    import torch
+
+    from taomate_hd_amd import SlotPool
+
+    pool = SlotPool(torch, heads=1, head_dim=64, device="cpu", max_free=2)
+    slots = [pool.acquire(n) for n in (64, 128, 192, 256)]
+    for s in slots:
+        pool.release(s)
+    assert len(pool._free) == 2 and sorted(s.capacity for s in pool._free) == [192, 256]
+    assert pool.free_bytes == sum(s.nbytes for s in pool._free)
+    assert pool.acquire(100) is slots[2]  # smallest free slot that fits
+
+
+def test_row_lists_are_range_checked_before_the_int32_cast_without_gpu():
+    import torch
+
+    from taomate_hd_amd.attention import _row_list
+
+    with pytest.raises(ValueError, match=r"in \[0, 10\)"):
+        _row_list(torch, torch.tensor([0, 2 ** 32 + 3], dtype=torch.int64), "cpu", 10, "rows", False)
+    with pytest.raises(ValueError, match="int32 or int64"):
+        _row_list(torch, torch.tensor([0.0, 1.0]), "cpu", 10, "rows", False)
+    rows = _row_list(torch, torch.tensor([3, 9], dtype=torch.int64), "cpu", 10, "rows", False)
+    assert rows.dtype == torch.int32 and rows.tolist() == [3, 9]

@@ -285,6 +285,33 @@ def test_hook_oracle_visibility_hand_derived():
         h("a", q, k, v, tags, mask, bounds, 0.5)
 
 
+def test_hook_oracle_condition_cache_hand_derived():
+    """Cached condition attention (attention_hook.py:445-465): the document's
+    condition query rows read zero, its media rows are unchanged (they still
+    attend over the condition keys); the compact output holds the kept rows
+    in order, and a kept row nobody writes stays zero."""
+    rng = np.random.default_rng(8)
+    T, Hh, Dd = 10, 1, 8
+    q, k, v = (rng.standard_normal((T, Hh, Dd)).astype(np.float32) for _ in range(3))
+    tags = np.array([1, 1, 1, 2, 0, 0, 0, -1, -1, -1])
+    mask = np.array([False] * 3 + [True] * 4 + [False] * 3)
+    bounds = (0, 7, 10)
+    c = ost.CacheOracle(("a",))
+    h = ost.HookOracle(c)
+    h.activate("noisy", 0)
+    full = h("a", q, k, v, tags, mask, bounds, 0.5)
+    cached = h("a", q, k, v, tags, mask, bounds, 0.5, cached_documents=(0,))
+    assert np.all(cached[:3] == 0) and np.array_equal(cached[3:], full[3:])
+    media_want = oatt.attention_fp64(q[3:7], k[:7], v[:7], 0.5)  # condition keys stay visible
+    np.testing.assert_allclose(cached[3:7], media_want, atol=1e-12)
+    assert np.array_equal(h("a", q, k, v, tags, mask, bounds, 0.5, cached_documents=(1,)), full)  # not live
+    kept = [3, 4, 5, 6, 8, 9]
+    compact = h("a", q, k, v, tags, mask, bounds, 0.5, cached_documents=(0,), compact_rows=kept)
+    assert compact.shape == (6, Hh, Dd) and np.array_equal(compact, full[kept])
+    with_cond = h("a", q, k, v, tags, mask, bounds, 0.5, cached_documents=(0,), compact_rows=[1, 4, 9])
+    assert np.all(with_cond[0] == 0) and np.array_equal(with_cond[1:], full[[4, 9]])
+
+
 # ---------------------------------------------------------------- QK norm + RoPE
 from oracle import rope as orope  # noqa: E402
 
