@@ -255,6 +255,66 @@ int tmhd_apply_rope(const void *value, int32_t tokens, int32_t heads, int32_t he
                     void *stream);
 
 /*
+ * Ulysses sequence <-> heads layouts (the all-to-all itself is the caller's).
+ * A rank holds `tokens` (T) tokens of the sequence with all `heads` (H)
+ * heads; after the exchange it holds all U*T tokens of L = ceil(H / U)
+ * heads, heads H..U*L-1 being zero padding.  head_dim (D) 64 or 128; world
+ * (U) 1..64; buffers and rows 16-byte aligned; outputs may not overlap inputs.
+ *
+ * tmhd_ulysses_qkv_send: merged projection qkv[T][3][H][D] (row stride
+ * row_stride elements) -> the send buffer of the sequence -> heads exchange:
+ *   layout 0: out[U][3][T][L][D]   the reference's layout
+ *   layout 1: out[U][T][3][L][D]   token-major: the received buffer is then
+ *             a merged projection of the U*T tokens (row stride 3*L*D) whose
+ *             Q / K / V thirds the hook reads in place (no receive copy)
+ * out[dest][part][t][l] = qkv[t][part][dest*L + l] (zero for padded heads).
+ * Replaces qkv_send_layout / _qkv_send,
+ * src/taomate_hd/distributed/ulysses_layout.py:9-41, as called by
+ * merged_qkv_sequence_to_heads (ulysses.py:183-212).
+ */
+int tmhd_ulysses_qkv_send(const void *qkv, int64_t row_stride, int32_t tokens, int32_t heads,
+                          int32_t head_dim, int32_t world, int32_t layout, void *out, void *stream);
+
+/*
+ * tmhd_qkv_norm_rope and tmhd_ulysses_qkv_send in one pass: the normalised,
+ * rotated Q / K rows go straight into the send buffer (qkv itself is left
+ * unchanged); V and the padding come from the plain send.  Same results as
+ * the two calls in sequence, bit for bit.  Replaces fused_qkv_qk_norm_rope_
+ * (fused_kernels.py:824-873) followed by merged_qkv_sequence_to_heads's send
+ * layout (ulysses.py:183-212) in MiniMaxH3Attention.forward (layers.py:400-438).
+ */
+int tmhd_ulysses_qkv_norm_rope_send(const void *qkv, int64_t row_stride, int32_t tokens,
+                                    int32_t heads, int32_t head_dim, const void *q_weight,
+                                    const void *k_weight, const void *cos_sin,
+                                    int64_t cos_sin_stride, int64_t cos_sin_rows,
+                                    int32_t rotary_dim, const int64_t *positions, float eps,
+                                    int32_t world, int32_t layout, void *out, void *stream);
+
+/*
+ * The received layout-0 buffer recv[U][3][T][L][D] (source rank, part, token,
+ * local head) -> out[U*T][3][L][D], row s*T + t at out + (s*T + t) *
+ * out_row_stride.  Replaces outputs.movedim(0, 1).contiguous() of
+ * merged_qkv_sequence_to_heads (ulysses.py:209-211), in the merged-row form
+ * the hook reads.
+ */
+int tmhd_ulysses_qkv_receive(const void *recv, int32_t tokens, int32_t local_heads,
+                             int32_t head_dim, int32_t world, void *out,
+                             int64_t out_row_stride, void *stream);
+
+/*
+ * The heads -> sequence direction: the received attention output
+ * recv[U][T][L][D] (source rank s holds heads s*L..) -> out[t][h][d] at
+ * out + t*out_token_stride + h*out_head_stride + d for h < heads (the
+ * padded heads are dropped).  Replaces attention_receive_layout /
+ * _attention_receive, ulysses_layout.py:44-67, as called by
+ * heads_to_sequence (ulysses.py:113-138).
+ */
+int tmhd_ulysses_attention_receive(const void *recv, int32_t tokens, int32_t heads,
+                                   int32_t head_dim, int32_t world, void *out,
+                                   int64_t out_token_stride, int64_t out_head_stride,
+                                   void *stream);
+
+/*
  * Row-wise bf16 ops of the DiT block around each attention call: `rows`
  * rows of `cols` columns (row strides in elements), bf16 weight [cols],
  * bf16 tables scale / shift / gate [table_rows][*] read at row t =

@@ -30,6 +30,12 @@ int kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_str
             int32_t vt_row_stride, int32_t dst, int32_t zero_to, int32_t heads, int32_t head_dim, void *stream,
             bool with_k, bool check_only);
 
+// The Ulysses send layout of a merged QKV projection (tmhd_ulysses_qkv_send)
+// for the parts whose bit is set in copy_parts (padded heads are always
+// zeroed); check_only validates the arguments and launches nothing.
+int ulysses_send(const void *qkv, int64_t row_stride, int32_t tokens, int32_t heads, int32_t head_dim,
+                 int32_t world, int32_t layout, void *out, int32_t copy_parts, void *stream, bool check_only);
+
 // bf16 bits -> fp32 (exact).
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);

@@ -58,6 +58,11 @@ struct RopeArgs {
   uint16_t *kslot;
   int64_t kslot_hs;
   int32_t stage_row0, stage_n, stage_dst;
+  // SEND only: rows go to the Ulysses send buffer instead of back in place:
+  // row (t, part p, head h) at ((dest * 3 + p) * tokens + t) * L + l (layout 0)
+  // or ((dest * tokens + t) * 3 + p) * L + l (layout 1), dest = h / L, l = h % L
+  uint16_t *send;
+  int32_t send_local, send_layout;
 };
 
 constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad in the inverse RMS pass
@@ -66,7 +71,8 @@ constexpr int kRopeUnroll = 4;  // row groups per wave; one per lane of a quad i
 // (the merged-projection form); otherwise at cos[t][d] and sin[t][d].
 // NORM false: the rotation alone, applied to the input values (no RMSNorm).
 // STAGE: the K rows of the staged token range also go to the slot.
-template <int D, bool TABLE, bool NORM = true, bool STAGE = false>
+// SEND: the rows go to the Ulysses send buffer (the source is left as it is).
+template <int D, bool TABLE, bool NORM = true, bool STAGE = false, bool SEND = false>
 __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
 #pragma clang fp contract(off)
   constexpr int LPR = D / 8;     // lanes per row
@@ -97,7 +103,15 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
     part_row[u] = r;
     is_k[u] = r >= a.heads;
     src_off[u] = (int64_t)t * a.src_stride + (int64_t)r * D;
-    dst_off[u] = (int64_t)t * a.dst_stride + (int64_t)r * D;
+    if constexpr (SEND) {
+      const int p = is_k[u] ? 1 : 0, h = r - p * a.heads;
+      const int dest = h / a.send_local, l = h - dest * a.send_local;
+      const int64_t row = a.send_layout == 0 ? (int64_t)(dest * 3 + p) * a.tokens + t
+                                             : ((int64_t)dest * a.tokens + t) * 3 + p;
+      dst_off[u] = (row * a.send_local + l) * D;
+    } else {
+      dst_off[u] = (int64_t)t * a.dst_stride + (int64_t)r * D;
+    }
     if (TABLE && a.rotary) pos[u] = a.pos[t];  // issued first: the cos / sin loads wait only for these
   }
   i32x2 xa[U], xb[U], ca[U], sa[U], cb[U], sb[U];
@@ -197,8 +211,9 @@ __global__ void __launch_bounds__(256) qk_norm_rope_kernel(const RopeArgs a) {
       }
     }
     if (live[u]) {
-      *(i32x2 *)(a.dst + dst_off[u] + oa) = i32x2{(int)out[0], (int)out[1]};
-      *(i32x2 *)(a.dst + dst_off[u] + ob) = i32x2{(int)out[2], (int)out[3]};
+      uint16_t *const dst = SEND ? a.send : a.dst;
+      *(i32x2 *)(dst + dst_off[u] + oa) = i32x2{(int)out[0], (int)out[1]};
+      *(i32x2 *)(dst + dst_off[u] + ob) = i32x2{(int)out[2], (int)out[3]};
       if constexpr (STAGE) {
         const int i = tok[u] - a.stage_row0;
         if (is_k[u] && i >= 0 && i < a.stage_n) {
@@ -219,13 +234,18 @@ int rope_rows_check(const RopeArgs &a, int head_dim, const char *what) {
 }
 
 int launch_rope(const RopeArgs &a, int head_dim, bool table, void *stream, const char *what, bool norm = true,
-                bool stage = false) {
+                bool stage = false, bool send = false) {
   if (int st = rope_rows_check(a, head_dim, what)) return st;
   const int64_t rows = (int64_t)a.tokens * a.parts * a.heads;
   const int rows_per_block = 4 * kRopeUnroll * (64 / (head_dim / 8));
   const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block)), block(256);
   hipStream_t s = (hipStream_t)stream;
-  if (stage) {
+  if (send) {
+    if (head_dim == 128)
+      hipLaunchKernelGGL((qk_norm_rope_kernel<128, true, true, false, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((qk_norm_rope_kernel<64, true, true, false, true>), grid, block, 0, s, a);
+  } else if (stage) {
     if (head_dim == 128)
       hipLaunchKernelGGL((qk_norm_rope_kernel<128, true, true, true>), grid, block, 0, s, a);
     else
@@ -401,4 +421,26 @@ extern "C" int tmhd_apply_rope(const void *value, int32_t tokens, int32_t heads,
              (const uint16_t *)cos, (const uint16_t *)sin, cos_stride, sin_stride, nullptr, 0, tokens, heads, 1,
              rotary_dim, 0.0f};
   return launch_rope(a, head_dim, false, stream, what, false);
+}
+
+extern "C" int tmhd_ulysses_qkv_norm_rope_send(const void *qkv, int64_t row_stride, int32_t tokens, int32_t heads,
+                                              int32_t head_dim, const void *q_weight, const void *k_weight,
+                                              const void *cos_sin, int64_t cos_sin_stride, int64_t cos_sin_rows,
+                                              int32_t rotary_dim, const int64_t *positions, float eps,
+                                              int32_t world, int32_t layout, void *out, void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_ulysses_qkv_norm_rope_send";
+  RopeArgs a{};
+  if (int st = qkv_rope_args(&a, const_cast<void *>(qkv), tokens, heads, head_dim, row_stride, q_weight, k_weight,
+                             cos_sin, cos_sin_stride, cos_sin_rows, rotary_dim, positions, eps, what))
+    return st;
+  // V rows and the zero padding heads come from the plain send (checked before any launch)
+  if (int st = ulysses_send(qkv, row_stride, tokens, heads, head_dim, world, layout, out, 4, stream, true)) return st;
+  if (tokens == 0) return TMHD_OK;
+  a.dst = nullptr;
+  a.send = (uint16_t *)out;
+  a.send_local = (heads + world - 1) / world;
+  a.send_layout = layout;
+  if (int st = launch_rope(a, head_dim, true, stream, what, true, false, true)) return st;
+  return ulysses_send(qkv, row_stride, tokens, heads, head_dim, world, layout, out, 4, stream, false);
 }

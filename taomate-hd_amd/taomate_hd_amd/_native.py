@@ -140,6 +140,22 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
             c_int32, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int32, c_int32, c_int32, c_void_p,
         ],
     ),
+    "tmhd_ulysses_qkv_send": (
+        c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32, c_void_p, c_void_p],
+    ),
+    "tmhd_ulysses_qkv_norm_rope_send": (
+        c_int,
+        [
+            c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+            c_int32, c_void_p, c_float, c_int32, c_int32, c_void_p, c_void_p,
+        ],
+    ),
+    "tmhd_ulysses_qkv_receive": (
+        c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_int64, c_void_p],
+    ),
+    "tmhd_ulysses_attention_receive": (
+        c_int, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p, c_int64, c_int64, c_void_p],
+    ),
     "tmhd_k_fixed_sum": (c_int, [c_void_p, c_int64, c_int32, c_int32, c_int32, c_void_p, c_void_p]),
     "tmhd_token_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int64, c_void_p]),
     "tmhd_weight_quant_i8": (c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p]),

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
 
     lib = _native.load()
     declared = _declared_symbols()
-    assert len(declared) == 27
+    assert len(declared) == 31
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED_SYMBOLS)
@@ -361,7 +361,7 @@ def test_w8a8_workspace_storage_without_gpu():
     q, s = ws.activations(x)
     assert q.dtype == torch.int8 and tuple(q.shape) == (100, 256)
     assert s.dtype == torch.float32 and tuple(s.shape) == (100, 1)
-    assert s.data_ptr() % 256 == 0 and s.data_ptr() >= q.data_ptr() + q.numel()
+    assert (s.data_ptr() - q.data_ptr()) % 256 == 0 and s.data_ptr() >= q.data_ptr() + q.numel()
     q2, _ = ws.activations(torch.zeros((10, 512)))  # smaller: same arena
     assert q2.data_ptr() == q.data_ptr()
     a = ws.output(x, 384)

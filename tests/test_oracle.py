@@ -563,3 +563,41 @@ def test_swiglu_closed_forms():
     assert out[0, 0] == 0.0 and out[0, 1] == 40.0 and abs(out[0, 2]) < 1e-6
     want = 1.0 / (1.0 + np.exp(-1.0))  # silu(1) = sigmoid(1)
     assert abs(out[0, 3] - want) <= 2.0 ** -8 * want
+
+
+# ---------------------------------------------------------------- Ulysses layouts
+from oracle import ulysses as oul  # noqa: E402
+
+
+@pytest.mark.parametrize("heads,world", [(8, 2), (28, 4), (7, 2), (10, 4), (5, 4), (3, 1)])
+def test_ulysses_layouts_round_trip_and_reshape_form(heads, world):
+    rng = np.random.default_rng(heads * 10 + world)
+    dim, tokens = 8, 5
+    local = oul.local_heads(heads, world)
+    # every rank's merged projection; values tag (rank, token, part, head, channel)
+    x = [rng.standard_normal((tokens, 3 * heads * dim)).astype(np.float32) for _ in range(world)]
+    sends = [oul.qkv_send(xi, heads, dim, world) for xi in x]
+    if heads % world == 0:
+        for xi, si in zip(x, sends):
+            assert np.array_equal(si, oul.qkv_send_reshape(xi, heads, dim, world))
+    for si in sends:  # padded heads are zero
+        pad = world * local - heads
+        if pad:
+            assert not si[-1, :, :, local - pad:].any()
+    received = oul.all_to_all(sends)
+    full = np.concatenate(x).reshape(world * tokens, 3, heads, dim)  # the whole sequence, rank order
+    for r in range(world):
+        q, k, v = oul.qkv_receive(received[r])
+        for p, part in enumerate((q, k, v)):
+            for l in range(local):
+                head = r * local + l
+                want = full[:, p, head] if head < heads else np.zeros((world * tokens, dim), np.float32)
+                assert np.array_equal(part[:, l], want)
+        tm = oul.all_to_all([oul.qkv_send_token_major(xi, heads, dim, world) for xi in x])[r]
+        assert np.array_equal(tm.reshape(world * tokens, 3, local, dim).transpose(1, 0, 2, 3), np.stack([q, k, v]))
+    # heads -> sequence: each rank's attention output over all tokens of its heads comes back
+    outs = [oul.qkv_receive(received[r])[0] for r in range(world)]  # [U*T, L, D] per rank
+    back = oul.all_to_all([o.reshape(world, tokens, local, dim) for o in outs])
+    for r in range(world):
+        got = oul.attention_receive(back[r], heads)
+        assert np.array_equal(got, x[r].reshape(tokens, 3, heads, dim)[:, 0])
