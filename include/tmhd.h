@@ -133,6 +133,23 @@ int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream);
 int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim);
 
 /*
+ * tmhd_attn_fwd_bf16 that allocates nothing: args->split_workspace must be
+ * NULL, and the key-range partials of a split last round go to a static
+ * device array of the library (33,816,576 bytes per device: one
+ * [256][head_dim + 1] fp32 slot for each CU of a device with up to 256 CUs;
+ * a device with more CUs is refused with TMHD_ERR_UNSUPPORTED).  Same
+ * results as tmhd_attn_fwd_bf16 with a workspace of
+ * tmhd_attn_split_workspace_bytes, bit for bit.  Every call on one GPU
+ * shares that array: calls ordered on one stream are safe, calls that
+ * overlap on one GPU (other streams) race.  The first call on a device
+ * looks up the array's address there.
+ * Has no counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).
+ */
+int tmhd_attn_fwd_bf16_noalloc(const tmhd_attn_args *args, void *stream);
+
+/*
  * INT8-QK streaming attention: int8 Q.K^T (int32 accumulate) dequantised by
  * the per-block scales, fp32 online softmax, bf16 P.V with fp32 accumulate.
  * Replaces sageattn_qk_int8_pv_fp8_cuda_sm90 / sage_with_fused_value_padding,

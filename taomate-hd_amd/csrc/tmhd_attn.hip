@@ -52,9 +52,17 @@
 // Scores of consecutive sub-tiles alternate between two register sets.
 #include <math.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "tmhd_internal.h"
+
+// Scratch of tmhd_attn_fwd_bf16_noalloc: the key-range partials of a split
+// last round, sized for one [256 rows][128 + 1] fp32 slot per CU of a
+// 256-CU device (33,816,576 bytes, held by every device the library runs on
+// until the process ends).  Host code reaches it only through the address
+// hipGetSymbolAddress gives per device (static_scratch below).
+static __device__ __align__(256) unsigned char scratch[256 * 256 * (128 + 1) * 4];
 
 namespace tmhd {
 namespace {
@@ -1064,8 +1072,54 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   return check_launch(what);
 }
 
+// Device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept; nullptr with the error
+// recorded if the lookup fails.
+void *static_scratch(const char *what) {
+  static std::mutex mu;
+  static void *addr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    set_error(TMHD_ERR_HIP, "%s: no current device", what);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error(TMHD_ERR_HIP, "%s: scratch address on device %d: %s", what, dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    addr[dev] = p;
+  }
+  return addr[dev];
+}
+
 }  // namespace
 }  // namespace tmhd
+
+extern "C" int tmhd_attn_fwd_bf16_noalloc(const tmhd_attn_args *args, void *stream) {
+  using namespace tmhd;
+  const char *what = "tmhd_attn_fwd_bf16_noalloc";
+  if (!args) return set_error(TMHD_ERR_INVALID, "%s: null args", what);
+  if (args->split_workspace)
+    return set_error(TMHD_ERR_INVALID, "%s: split_workspace must be NULL (the library's static scratch is used)",
+                     what);
+  KArgs k;
+  if (int st = build_kargs(args, nullptr, false, &k)) return st;
+  // any call's split needs at most one slot per CU of the device
+  const int64_t need = (int64_t)device_cus() * split_slot_bytes(args->head_dim);
+  if (need > (int64_t)sizeof(scratch))
+    return set_error(TMHD_ERR_UNSUPPORTED, "%s: %lld bytes of split scratch on this device exceed the static %lld",
+                     what, (long long)need, (long long)sizeof(scratch));
+  void *ws = static_scratch(what);
+  if (!ws) return TMHD_ERR_HIP;
+  tmhd_attn_args a = *args;
+  a.split_workspace = ws;
+  a.split_workspace_bytes = (int64_t)sizeof(scratch);
+  return launch_attn<false>(&a, nullptr, stream);
+}
 
 extern "C" int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim) {
   if (head_dim != 64 && head_dim != 128) return 0;

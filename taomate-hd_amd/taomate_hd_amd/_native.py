@@ -80,6 +80,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "tmhd_last_error": (c_char_p, []),
     "tmhd_attn_split_workspace_bytes": (c_int64, [c_int32]),
     "tmhd_attn_fwd_bf16": (c_int, [POINTER(AttnArgs), c_void_p]),
+    "tmhd_attn_fwd_bf16_noalloc": (c_int, [POINTER(AttnArgs), c_void_p]),
     "tmhd_attn_fwd_i8qk": (c_int, [POINTER(AttnArgs), POINTER(QKQuant), c_void_p]),
     "tmhd_qk_smooth_quant": (c_int, [POINTER(AttnArgs), POINTER(QKQuant), c_void_p]),
     "tmhd_kv_pack": (

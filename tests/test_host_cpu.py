@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
 
     lib = _native.load()
     declared = _declared_symbols()
-    assert len(declared) == 31
+    assert len(declared) == 32
     for name in declared:
         assert hasattr(lib, name), name
     assert set(declared) == set(_native.EXPORTED_SYMBOLS)
