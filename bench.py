@@ -7,15 +7,17 @@ video anchor (4,032 tokens) and two 12,252-token history chunks, read in
 place from the cache's slots, plus the chunk's own 12,252 keys/values, which
 the hook packs into a slot first.  H = 40, D = 128, no mask; Q/K/V ~ N(0, 1)
 bf16 with a per-(head, channel) key offset ~ N(0, 0.5), synthetic data.
-The same step with the INT8-QK backend and the W8A8 projection
-(12,252 x 5,120 -> 13,824, per-token INT8 X, per-channel INT8 W, bf16 bias)
-are measured beside it and reported in the same JSON line, together with the
-reference's own serial backend (dense K/V + torch SDPA) on the same GPU and
-inputs, the DiT block's row ops around the call (Q/K norm + RoPE, RMSNorm /
-AdaLN / residual gate) and dense packed attention.
+The 480p-stage call (4,836 queries over 16,068 keys), the 768p step with
+the INT8-QK backend and the W8A8 projection (12,252 x 5,120 -> 13,824,
+per-token INT8 X, per-channel INT8 W, bf16 bias) are measured beside it and
+reported in the same JSON line, together with the reference's own serial
+backend (dense K/V + torch SDPA) on the same GPU and inputs, the DiT block's
+row ops around the call (Q/K norm + RoPE, RMSNorm / AdaLN / residual gate),
+the Ulysses send layouts, dense packed attention and the CPU baselines of the
+BF16, INT8-QK and W8A8 paths on the host cores.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload all|bf16|i8qk|w8a8|rope|adaln|packed|copy]
+                    [--workload all|bf16|c2|i8qk|w8a8|rope|adaln|packed|mlp|prep|faithful|ulysses|copy]
                     [--no-cpu-baseline] [--no-reference-gpu]
 """
 
@@ -48,6 +50,9 @@ HIDDEN = 5376
 LQ = 12252  # 3 latent frames x 48 x 84 video tokens + 156 audio tokens
 VIDEO, AUDIO = 12096, 156
 ANCHOR = 4032
+# 480p stage: 3 latent frames x 30 x 52 video tokens + 156 audio tokens, anchor 1,560
+LQ_480, VIDEO_480, ANCHOR_480 = 4836, 4680, 1560
+LKV_480 = LQ_480 + ANCHOR_480 + 2 * LQ_480  # 16,068
 LKV = LQ + ANCHOR + 2 * LQ  # 40,788
 ATTN_FLOPS = 4.0 * H * LQ * LKV * D
 LAYER = "blocks.0.attn"
@@ -56,7 +61,9 @@ FFN = 14336  # MLP width of the DiT (model/architecture.py:21)
 # the model's own 768p HIGH-stage hook call: 14 local heads (56 over TP2 x Ulysses 2),
 # chunk = 10 latents x 1,032 video tokens + 2 x 57 audio, sink = 12 latents of video
 FAITHFUL = dict(heads=14, anchor=12 * 1032, video=10 * 1032, audio=2 * 57)
-TRAFFIC_PROFILE = REPO / "profiles" / "attn_fwd_bf16_768p_pmc.txt"
+ATTN_SOURCE = REPO / "taomate-hd_amd" / "csrc" / "tmhd_attn.hip"
+GEMM_SOURCE = REPO / "taomate-hd_amd" / "csrc" / "tmhd_w8a8.hip"
+PEAK_MIXED_TFLOPS = PEAK_BF16_TFLOPS * 4.0 / 3.0  # INT8 Q.K^T at 2x the BF16 rate, BF16 P.V
 
 
 def _log(msg: str) -> None:
@@ -266,6 +273,43 @@ def bench_prep_hook(torch, dev, steps, warmup, cache, inputs):
     return {"separate": (a_ms + a2_ms) / 2, "staged": (b_ms + b2_ms) / 2}
 
 
+def bench_c2(torch, dev, steps, warmup):
+    """The 480p-stage layer call (BF16): 4,836 queries over the 1,560-token
+    anchor, two 4,836-token history chunks in the cache's slots and the
+    chunk's own 4,836 keys.  Returns (ms per call, attention kernel ms)."""
+    cache, inputs = build_stream(torch, dev, None, heads=H, anchor=ANCHOR_480, video=VIDEO_480, audio=AUDIO)
+    wall_ms, _, comps = bench_attention(torch, dev, "sdpa", steps, warmup, cache, inputs)
+    return wall_ms, comps["attention"]["mean_ms"], {k: round(v["mean_ms"], 4) for k, v in comps.items()}
+
+
+def bench_ulysses(torch, dev, steps, warmup, world=4):
+    """The Ulysses send of the 768p chunk's merged QKV projection (12,252 x
+    3 x 40 x 128) for a group of 4 (10 local heads per rank): the plain send,
+    and Q/K RMSNorm + RoPE written straight into the send buffer against
+    norm + RoPE in place then the send.  Returns {name: device ms per call}."""
+    from taomate_hd_amd import fused_qkv_qk_norm_rope_, ulysses
+
+    gen = torch.Generator(device=dev).manual_seed(13)
+    qkv = _randn(torch, (LQ, 3 * H * D), gen, dev).to(torch.bfloat16)
+    w = (1.0 + 0.1 * _randn(torch, (D,), gen, dev)).to(torch.bfloat16)
+    ang = _randn(torch, (4096, ROTARY // 2), gen, dev)
+    table = torch.cat([ang.cos(), ang.sin()], -1).to(torch.bfloat16)
+    pos = torch.arange(LQ, device=dev) % 4096
+    out = {}
+    for token_major in (False, True):
+        send = ulysses.qkv_send_layout(qkv, num_heads=H, head_dim=D, world_size=world, token_major=token_major)
+        tag = "token_major" if token_major else "reference_layout"
+        _, out[f"send_{tag}"] = time_steps(torch, lambda: ulysses.qkv_send_layout(
+            qkv, num_heads=H, head_dim=D, world_size=world, token_major=token_major, out=send), steps, warmup)
+    _, out["norm_rope_then_send"] = time_steps(torch, lambda: (fused_qkv_qk_norm_rope_(qkv, w, w, table, pos, 1e-6),
+                                                               ulysses.qkv_send_layout(qkv, num_heads=H, head_dim=D,
+                                                                                       world_size=world, token_major=True,
+                                                                                       out=send)), steps, warmup)
+    _, out["norm_rope_send"] = time_steps(torch, lambda: ulysses.qkv_norm_rope_send_layout(
+        qkv, w, w, table, pos, 1e-6, world_size=world, token_major=True, out=send), steps, warmup)
+    return out
+
+
 def bench_rope(torch, dev, steps, warmup):
     """Q/K RMSNorm + RoPE in place in the merged QKV projection of the 768p chunk
     (the step in front of the hook), synthetic bf16 inputs; returns ms per call."""
@@ -322,49 +366,157 @@ def bench_adaln(torch, dev, steps, warmup):
     return {"rms_norm_modulate": (pre_ms, 2 * row_bytes), "residual_gate_rms_norm_modulate": (post_ms, 4 * row_bytes)}
 
 
-def cpu_baseline(torch):
-    """The reference serial backend (torch SDPA, fp32) on the host cores over the 768p attention.
+def _cpu_threads(torch) -> dict:
+    """Use every host core this process may run on: os.cpu_count() shows the
+    host's cores, the CPU affinity the ones granted to the process, and a box
+    that shares its host sets OMP_NUM_THREADS to its share; the smallest of
+    these is used (torch.set_num_threads) and all three are recorded."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = min(c for c in (os.cpu_count(), affinity, int(omp) if omp and omp.isdigit() else None) if c)
+    torch.set_num_threads(threads)
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": affinity, "omp_num_threads": omp, "threads": threads}
 
-    Runs groups of 8 heads (Lq 12252 x Lkv 40788 each), cycling over the 40
-    heads, until about 12 s of CPU work has been timed (at most 30 s, at least
-    one group) and reports the aggregate rate."""
-    from oracle.attention import sdpa_cpu
 
-    threads = torch.get_num_threads()
-    gen = torch.Generator().manual_seed(0)
-    group = 8
-    q = torch.randn(LQ, group, D, generator=gen).to(torch.bfloat16).float()
-    k = torch.randn(LKV, group, D, generator=gen).to(torch.bfloat16).float()
-    v = torch.randn(LKV, group, D, generator=gen).to(torch.bfloat16).float()
+def _median_s(fn, runs: int = 3) -> float:
+    """1 warm-up, then the median wall time of ``runs`` runs."""
+    fn()
     times = []
-    while not times or (sum(times) < 12.0 and sum(times) + times[-1] <= 30.0):
+    for _ in range(runs):
         t0 = time.perf_counter()
-        sdpa_cpu(q, k, v, D ** -0.5)
+        fn()
         times.append(time.perf_counter() - t0)
-    heads_done = group * len(times)
-    total = sum(times)
-    flops = 4.0 * heads_done * LQ * LKV * D
+    return sorted(times)[len(times) // 2]
+
+
+def _cpu_attention_heads(torch, fn, lq, segs, gen, heads_list=(1, 4)):
+    """Median seconds of ``fn`` on 1 and 4 heads of one call's shapes."""
+    n = sum(segs)
+    out = {}
+    for hh in heads_list:
+        q = torch.randn(lq, hh, D, generator=gen).to(torch.bfloat16).float()
+        off = 0.5 * torch.randn(hh, D, generator=gen)
+        k = (torch.randn(n, hh, D, generator=gen) + off).to(torch.bfloat16).float()
+        v = torch.randn(n, hh, D, generator=gen).to(torch.bfloat16).float()
+        out[hh] = _median_s(lambda: fn(q, k, v))
+    return out
+
+
+def cpu_baseline(torch):
+    """The reference's CPU path on the host cores, BASELINE's protocol: 1
+    warm-up, median of 3 runs, 1 and 4 heads timed, the 40-head call
+    extrapolated linearly (marked as such).
+
+    * 768p BF16 (the metric's workload) and 480p BF16: torch SDPA in fp32,
+      the reference's serial backend;
+    * 768p INT8-QK: the CPU emulation of the quantized path (per-block INT8
+      Q / K after the smooth-K mean, exact integer Q.K^T in fp32, fp32
+      softmax and P.V);
+    * the W8A8 projection: token quant plus the exact fp64 GEMM and the
+      epilogue on a 512-row subset, extrapolated to 12,252 rows."""
+    import numpy as np
+
+    from oracle import quant as oq
+    from oracle.attention import i8qk_attention_cpu, sdpa_cpu
+
+    cpu = _cpu_threads(torch)
+    gen = torch.Generator().manual_seed(0)
+    t_start = time.perf_counter()
+    legs = {}
+
+    def attention_leg(name, lq, segs, fn, kind):
+        t = _cpu_attention_heads(torch, fn, lq, segs, gen)
+        lkv = sum(segs)
+        flops = 4.0 * H * lq * lkv * D
+        call_s = t[4] / 4 * H
+        legs[name] = {
+            "tflops": round(flops / call_s / 1e12, 4),
+            "ms_per_layer_call_extrapolated": round(call_s * 1e3, 1),
+            "s_1_head": round(t[1], 4),
+            "s_4_heads": round(t[4], 4),
+            "scaling_4_over_1": round(t[4] / t[1], 3),
+            "sample": f"{kind}: Lq {lq} x Lkv {lkv}, 1 and 4 of the 40 heads (median of 3 after 1 warm-up); "
+                      "the 40-head call extrapolated linearly from 4 heads",
+        }
+
+    sdpa = lambda q, k, v: sdpa_cpu(q, k, v, D ** -0.5)  # noqa: E731
+    attention_leg("bf16_768p", LQ, [ANCHOR, LQ, LQ, LQ], sdpa, "torch SDPA fp32 on CPU (reference serial backend)")
+    attention_leg("bf16_480p", LQ_480, [ANCHOR_480, LQ_480, LQ_480, LQ_480], sdpa,
+                  "torch SDPA fp32 on CPU (reference serial backend)")
+
+    def i8(q, k, v):
+        segs = [ANCHOR, LQ, LQ, LQ]
+        ks, off = [], 0
+        for c in segs:
+            ks.append(k[off : off + c])
+            off += c
+        return i8qk_attention_cpu(q, ks, v, D ** -0.5)
+
+    attention_leg("i8qk_768p", LQ, [ANCHOR, LQ, LQ, LQ], i8, "INT8-QK emulation in torch fp32 on CPU")
+    # W8A8: 512 rows of the projection
+    rng = np.random.default_rng(0)
+    rows = 512
+    x = rng.standard_normal((rows, K_X)).astype(np.float32)
+    x[:, rng.permutation(K_X)[: K_X // 100]] *= 20.0
+    w = (0.02 * rng.standard_normal((N_W, K_X))).astype(np.float32)
+    bias = (0.02 * rng.standard_normal(N_W)).astype(np.float32)
+    wq, ws = oq.weight_quant(w)  # load time, not timed
+
+    def w8a8():
+        xq, xs = oq.token_quant(x)
+        return oq.scaled_mm_epilogue(oq.int_gemm(xq, wq), xs, ws, bias)
+
+    t = _median_s(w8a8)
+    ops = 2.0 * M_X * N_W * K_X
+    legs["w8a8_projection"] = {
+        "tops": round(ops / (t * M_X / rows) / 1e12, 4),
+        "ms_per_projection_extrapolated": round(t * M_X / rows * 1e3, 1),
+        "s_512_rows": round(t, 4),
+        "sample": f"token quant + exact fp64 GEMM + epilogue (numpy) on {rows} of the {M_X} rows "
+                  f"({K_X} -> {N_W}), median of 3 after 1 warm-up; extrapolated linearly to {M_X} rows",
+    }
+    main = legs["bf16_768p"]
     return {
-        "value": round(flops / total / 1e12, 4),
+        "value": main["tflops"],
         "unit": "TFLOPS",
-        "cores": threads,
+        "cores": cpu["threads"],
         "kind": "port",
-        "sample": (
-            f"torch SDPA fp32 on CPU (reference serial backend), 768p shapes Lq {LQ} x Lkv {LKV}, "
-            f"{len(times)} groups of {group} heads ({heads_done / H:.2f} layer calls), {total:.1f} s of CPU work; "
-            f"whole-call equivalent {total * H / heads_done * 1e3:.0f} ms"
-        ),
+        "sample": main["sample"] + f"; whole-call equivalent {main['ms_per_layer_call_extrapolated']} ms",
+        "host": cpu,
+        "configs": legs,
+        "cpu_seconds_total": round(time.perf_counter() - t_start, 1),
     }
 
 
-def read_traffic():
-    """HBM bytes per attention launch from the committed rocprof counter summary, if any."""
-    if not TRAFFIC_PROFILE.exists():
-        return None
-    for line in TRAFFIC_PROFILE.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1].split()[0])
-    return None
+def source_sha16(path: Path) -> str:
+    import hashlib
+
+    return hashlib.sha256(path.read_bytes()).hexdigest()[:16]
+
+
+def read_traffic(profile: Path, source: Path) -> tuple[float | None, str]:
+    """HBM bytes per launch from a committed rocprof counter summary, when the
+    summary was made from the kernel source now in the tree (its
+    ``source_sha16`` line); otherwise None and the reason."""
+    if not profile.exists():
+        return None, f"no profile {profile.name}"
+    fields = {}
+    for line in profile.read_text().splitlines():
+        if ":" in line and not line.startswith("#"):
+            key, _, rest = line.partition(":")
+            fields[key.strip()] = rest.split()[0] if rest.split() else ""
+    if fields.get("source_sha16") != source_sha16(source):
+        return None, f"{profile.name} was made from another {source.name} (stale)"
+    try:
+        return float(fields["traffic_bytes_per_launch"]), f"profiles/{profile.name}"
+    except (KeyError, ValueError):
+        return None, f"{profile.name} has no traffic line"
+
+
+def roofline(achieved: float, peak: float, bound: str, unit: str, profile: str, source: Path, **extra) -> dict:
+    traffic, origin = read_traffic(REPO / "profiles" / profile, source)
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic, "traffic_source": origin, **extra}
 
 
 def main() -> int:
@@ -374,7 +526,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
-    ap.add_argument("--workload", choices=("all", "bf16", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep", "faithful", "copy"),
+    ap.add_argument("--workload", choices=("all", "bf16", "c2", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep",
+                                           "faithful", "ulysses", "copy"),
                     default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -449,18 +602,11 @@ def main() -> int:
         result["us_per_layer_call"] = round(wall_ms * 1e3, 1)
         result["frac_bf16_peak"] = round(result["value"] / PEAK_BF16_TFLOPS, 4)
         result["components_ms"] = {k: round(v["mean_ms"], 4) for k, v in comps.items()}
-        traffic = read_traffic()
-        result["roofline"] = {
-            "bound": "mfma",
-            "achieved": round(achieved, 2),
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": traffic,
-            "kernel": "attn_fwd_kernel<128, bf16> + attn_merge_kernel<128> (split last round)",
-            "flops_per_launch": ATTN_FLOPS,
-            "kernel_ms": round(attn_ms, 4),
-        }
+        result["roofline"] = roofline(
+            achieved, PEAK_BF16_TFLOPS, "mfma", "TFLOP/s", "attn_fwd_bf16_768p_pmc.txt", ATTN_SOURCE,
+            kernel="attn_fwd_kernel<128, bf16> + attn_merge_kernel<128> (split last round)",
+            flops_per_launch=ATTN_FLOPS, kernel_ms=round(attn_ms, 4),
+            timing="HIP events around each attention call on its launch stream, timed steps only")
         _log(f"bf16: {wall_ms:.3f} ms/step (device {dev_ms:.3f}), kernel {attn_ms:.3f} ms = {achieved:.1f} TFLOPS")
         if not args.no_reference_gpu:
             ref_ms = bench_reference_sdpa(torch, dev, min(args.steps, 5), 1, cache, inputs)
@@ -472,6 +618,23 @@ def main() -> int:
                 "speedup_of_value": round(ref_ms / wall_ms, 2),
             }
             _log(f"reference backend on this GPU: {ref_ms:.3f} ms per layer call")
+    if args.workload in ("all", "c2"):
+        c2_ms, c2_attn_ms, c2_comps = bench_c2(torch, dev, args.steps, args.warmup)
+        c2_flops = 4.0 * H * LQ_480 * LKV_480 * D
+        result["bf16_480p"] = {
+            "us_per_layer_call": round(c2_ms * 1e3, 1),
+            "tflops": round(c2_flops / (c2_ms * 1e-3) / 1e12, 2),
+            "frac_bf16_peak": round(c2_flops / (c2_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "kernel_tflops": round(c2_flops / (c2_attn_ms * 1e-3) / 1e12, 2),
+            "kernel_frac_bf16_peak": round(c2_flops / (c2_attn_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "components_ms": c2_comps,
+            "shape": f"H {H}, D {D}, Lq {LQ_480} over Lkv {LKV_480} = anchor {ANCHOR_480} + 2 x {LQ_480} history "
+                     f"(cache slots) + {LQ_480} self (packed per call)",
+        }
+        _log(f"bf16 480p: {c2_ms:.3f} ms per layer call, kernel {c2_attn_ms:.3f} ms")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["bf16_480p"]["tflops"], round(c2_ms, 4)
+        torch.cuda.empty_cache()
     if args.workload in ("all", "prep"):
         prep = bench_prep_hook(torch, dev, args.steps, args.warmup, cache, inputs)
         result["norm_rope_and_chunk_staging"] = {
@@ -500,6 +663,12 @@ def main() -> int:
             "note": "qk_quant sums the chunk's own keys each call; the cached blocks' exact key sums are kept "
                     "on their slots from the first (warm-up) call, as in streaming, where a committed block's "
                     "keys do not change between calls",
+            "roofline": roofline(
+                ATTN_FLOPS / (attn_ms * 1e-3) / 1e12, round(PEAK_MIXED_TFLOPS, 1), "mfma", "TFLOP/s",
+                "attn_fwd_i8qk_768p_pmc.txt", ATTN_SOURCE,
+                kernel="attn_fwd_kernel<128, i8> + attn_merge_kernel<128> (split last round)",
+                peak_note="mixed peak: INT8 Q.K^T at 5,033 TOPS and BF16 P.V at 2,517 TFLOPS, half the work each",
+                flops_per_launch=ATTN_FLOPS, kernel_ms=round(attn_ms, 4)),
         }
         if result["value"]:
             entry["speedup_vs_bf16"] = round(tflops / result["value"], 3)
@@ -543,6 +712,11 @@ def main() -> int:
             "gemm_frac_int8_peak": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
             "token_quant_us": round(quant_ms * 1e3, 1),
             "token_quant_frac_hbm": round(qbytes / (quant_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "roofline": roofline(
+                ops / (gemm_ms * 1e-3) / 1e12, PEAK_INT8_TOPS, "mfma", "TFLOP/s",
+                "gemm_w8a8_12252x5120x13824_pmc.txt", GEMM_SOURCE,
+                kernel="gemm_i8_wave128_kernel (+ its k-split last round and merge)", unit_note="TOPS (int8 ops)",
+                ops_per_launch=ops, kernel_ms=round(gemm_ms, 4)),
         }
         _log(f"w8a8: {wall_ms:.3f} ms/projection (device {w8_dev_ms:.3f}), gemm {gemm_ms:.3f} ms, quant {quant_ms:.3f} ms")
         if result["value"] is None:
@@ -586,6 +760,20 @@ def main() -> int:
         if result["value"] is None:
             result["value"], result["ms_per_step"] = result["packed_sdpa"]["tflops"], round(packed_ms, 4)
             result["unit"] = "TFLOPS"
+    if args.workload in ("all", "ulysses"):
+        ul = bench_ulysses(torch, dev, args.steps, args.warmup)
+        moved = 2.0 * 2.0 * LQ * 3 * H * D  # bytes read + written by the send (no padded heads at 40 / 4)
+        result["ulysses_send_768p"] = {
+            **{f"{k}_us": round(v * 1e3, 1) for k, v in ul.items()},
+            "send_gbps": round(moved / (ul["send_token_major"] * 1e-3) / 1e9, 1),
+            "send_frac_hbm": round(moved / (ul["send_token_major"] * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+            "shape": f"merged QKV {LQ} x {3 * H * D}, Ulysses group of 4 (10 local heads), rotary {ROTARY}",
+        }
+        _log(f"ulysses send: {ul}")
+        if result["value"] is None:
+            result["value"], result["ms_per_step"] = result["ulysses_send_768p"]["send_gbps"], round(
+                ul["send_token_major"], 4)
+            result["unit"] = "GB/s"
     if args.workload in ("all", "mlp"):
         mlp = bench_mlp(torch, dev, args.steps, args.warmup)
         ops = 2.0 * LQ * HIDDEN * 2 * FFN
@@ -601,6 +789,7 @@ def main() -> int:
             result["value"], result["ms_per_step"] = result["mlp_fc1_swiglu"]["fused_tops"], round(mlp["fused"], 4)
             result["unit"] = "TOPS"
     if not args.no_cpu_baseline and args.workload in ("all", "bf16"):
+        torch.cuda.empty_cache()
         result["cpu_baseline"] = cpu_baseline(torch)
         _log(f"cpu baseline: {result['cpu_baseline']}")
     print(json.dumps(result), flush=True)

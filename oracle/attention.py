@@ -3,6 +3,7 @@
 * ``attention_fp64``   exact softmax(q k^T * scale) v in float64
 * ``sdpa_cpu``         the reference's serial backend, torch SDPA on CPU fp32
 * ``i8qk_attention``   the INT8-QK (SageAttention-style) arithmetic in float64
+* ``i8qk_attention_cpu`` the same arithmetic in torch fp32 (the timed CPU baseline)
 """
 
 from __future__ import annotations
@@ -98,6 +99,44 @@ def i8qk_attention(q: np.ndarray, k_segments: list[np.ndarray], v_segments: list
         p /= p.sum(axis=1, keepdims=True)
         out[:, h, :] = p @ v_all[:, h, :]
     return out, {"mean": mean, "k_i8": kq, "k_scale": ks, "q_i8": qq, "q_scale": qs}
+
+
+def i8qk_attention_cpu(q, k_segments, v, scale: float):
+    """The INT8-QK arithmetic on CPU torch fp32 tensors, as the timed CPU
+    baseline of the quantized path: the same smooth-K mean and per-128-block
+    quantization as ``i8qk_attention`` (fp32 mean of bf16 keys, rounded to
+    bf16; q_i8 = sat(rint(x * (127 / amax)))), the integer Q.K^T in fp32 (exact:
+    |q_i8 . k_i8| <= 127^2 * 128 < 2^24), then fp32 softmax and P.V.
+    ``q [Lq, H, D]``, ``k_segments`` a list of ``[n_i, H, D]``, ``v [N, H, D]``
+    (fp32 tensors holding bf16 values).  Returns ``[Lq, H, D]`` fp32.
+    Pinned by tests/test_oracle.py against ``i8qk_attention`` (fp64).
+    """
+    import torch
+
+    def block_quant(x):
+        n, h, d = x.shape
+        nb = (n + 127) // 128
+        pad = torch.zeros((nb * 128 - n, h, d), dtype=x.dtype)
+        xb = torch.cat([x, pad]).view(nb, 128, h, d)
+        amax = xb.abs().amax(dim=(1, 3))  # [nb, H]
+        # tensor / tensor: torch's scalar / tensor form is not correctly rounded on CPU
+        inv = torch.where(amax > 0, torch.full_like(amax, 127.0) / amax, torch.zeros_like(amax))
+        qi = torch.clamp(torch.round(xb * inv[:, None, :, None]), -128, 127)
+        return qi.view(nb * 128, h, d)[:n], (amax / 127.0).repeat_interleave(128, 0)[:n]  # [n, H]
+
+    keys = torch.cat(list(k_segments))
+    mean = (keys.double().sum(0) / keys.shape[0]).float().to(torch.bfloat16).float()
+    qq, qs = block_quant(q)
+    parts = []
+    for k in k_segments:
+        kq, ks = block_quant(k - mean)
+        parts.append((kq, ks))
+    out = torch.empty_like(q)
+    for h in range(q.shape[1]):
+        logits = torch.cat([(qq[:, h] @ kq[:, h].T) * ks[None, :, h] for kq, ks in parts], dim=1)
+        logits *= qs[:, h, None] * scale
+        out[:, h] = torch.softmax(logits, dim=1) @ v[:, h]
+    return out
 
 
 def cosine(a: np.ndarray, b: np.ndarray) -> float:

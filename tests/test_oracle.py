@@ -207,6 +207,19 @@ def test_i8qk_attention_algebra():
     assert oatt.cosine(out, exact) > 0.999
 
 
+def test_i8qk_cpu_baseline_equals_the_fp64_emulation():
+    import torch
+
+    q = _rand((300, 2, 64), 45)
+    kseg = [_rand((200, 2, 64), 46) + 0.4, _rand((77, 2, 64), 47)]
+    vseg = [_rand((200, 2, 64), 48), _rand((77, 2, 64), 49)]
+    want, _ = oatt.i8qk_attention(q, kseg, vseg, 0.125)
+    got = oatt.i8qk_attention_cpu(torch.from_numpy(q), [torch.from_numpy(k) for k in kseg],
+                                  torch.from_numpy(np.concatenate(vseg)), 0.125).numpy()
+    # same quantized operands: only fp32 rounding of the softmax and P.V differs
+    np.testing.assert_allclose(got, want, atol=2e-6)
+
+
 # ---------------------------------------------------------------- stream semantics
 def test_packed_layout_hand_derived():
     tags, mask, bounds = ost.packed_layout(3, 2, 2, 4, align=8)
