@@ -406,3 +406,51 @@ def test_i8qk_key_sum_memo_hits_and_invalidation(torch_mod, dev):
     assert torch.equal(third[1].view(torch.int16), fresh[1].view(torch.int16))
     assert not torch.equal(third[1].view(torch.int16), first[1].view(torch.int16))
     assert torch.equal(third[0].view(torch.int16), fresh[0].view(torch.int16))
+
+
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_plumbing_config_exact_inputs_through_the_hook(torch_mod, dev, backend):
+    """The CPU-runnable plumbing configuration exactly: batch 1, 8 heads, head_dim
+    64, 256 chunk queries over 1,024 keys (768 cached history + 256 self), no
+    mask, Q / K / V ~ N(0, 1) fp32 then cast to bf16 with torch generators
+    seeded 0 (Q), 1 (K) and 2 (V), no key offset; one noisy hook call over a
+    cache holding the 768 history keys, against torch SDPA on the CPU (the
+    reference's serial backend) and the fp64 oracle."""
+    torch = torch_mod
+    from oracle.attention import sdpa_cpu
+    from taomate_hd_amd import HeadMajorRingKVCache, HookMode, KVContract, StreamingAttentionHook
+
+    H, D, LQ, HIST = 8, 64, 256, 768
+
+    def draw(seed, rows):
+        return torch.randn(rows, H, D, generator=torch.Generator().manual_seed(seed), dtype=torch.float32)
+
+    q = draw(0, LQ).to(torch.bfloat16)
+    k = draw(1, HIST + LQ).to(torch.bfloat16)
+    v = draw(2, HIST + LQ).to(torch.bfloat16)
+    layer = "blocks.0.attn"
+    cache = HeadMajorRingKVCache(KVContract(layer_names=(layer,), local_heads=H, head_dim=D))
+    cache.begin_clean_commit(0)
+    tags = torch.tensor([2] * 16 + [0] * (HIST - 16), device=dev)
+    cache.stage(layer, k[:HIST].to(dev), v[:HIST].to(dev), tags, torch.ones(HIST, dtype=torch.bool, device=dev))
+    cache.commit()
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
+    hook.activate(mode=HookMode.NOISY, block_index=1)
+
+    class Attn:
+        softmax_scale = D ** -0.5
+
+    out = hook(attention=Attn(), layer_name=layer, query=q.to(dev), key=k[HIST:].to(dev), value=v[HIST:].to(dev),
+               token_tags=torch.tensor([2] * 16 + [0] * (LQ - 16), device=dev),
+               commit_mask=torch.ones(LQ, dtype=torch.bool, device=dev), cu_seqlens=None,
+               cu_seqlens_host=(0, LQ), max_seqlen=LQ)
+    torch.cuda.synchronize()
+    got = bf16.from_torch(out)
+    ref = sdpa_cpu(q.float(), k.float(), v.float(), D ** -0.5).numpy()
+    exact = oatt.attention_fp64(bf16.from_torch(q), bf16.from_torch(k), bf16.from_torch(v), D ** -0.5)
+    if backend == "sdpa":
+        for want in (ref, exact):
+            mx, mean = err_stats(got, want)
+            assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+    else:
+        assert oatt.cosine(got, ref) >= I8_COSINE and oatt.cosine(got, exact) >= I8_COSINE
