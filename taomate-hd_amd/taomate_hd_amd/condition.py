@@ -43,6 +43,9 @@ class ConditionLayerState:
     ``compact_rows``     None, or the sorted global rows kept in the compact
                          order (host sequence): the hook's output then has
                          one row per kept row, in that order.
+    ``attention_output_compact`` becomes True once the hook has taken a compact
+    writer for this layer (the flag the reference sets on its layer plan,
+    condition_cache.py:224), so the caller knows the output's row order.
     """
 
     def __init__(self, layer: str, cached_documents: Iterable[int] = (), compact_rows: Iterable[int] | None = None,
@@ -50,6 +53,7 @@ class ConditionLayerState:
         self.layer = str(layer).removesuffix(".attn")
         self.cached_documents = frozenset(int(d) for d in cached_documents)
         self.compact_rows = None
+        self.attention_output_compact = False
         self._to_compact: np.ndarray | None = None
         self._device_rows: dict[tuple[Any, ...], Any] = {}
         if compact_rows is not None:
@@ -147,6 +151,7 @@ def compact_condition_attention_output(layer_name: str, query: Any) -> CompactAt
     state = _ACTIVE.get()
     if state is None or state.compact_rows is None or not state.matches(layer_name):
         return None
+    state.attention_output_compact = True
     return CompactAttentionOutput(state, query)
 
 

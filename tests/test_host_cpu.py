@@ -320,7 +320,9 @@ def test_condition_cache_queries_and_compact_writer_without_gpu():
     state = condition.ConditionLayerState("blocks.0.attn", cached_documents=(0,), compact_rows=[2, 3, 5, 7, 8, 9])
     with condition.condition_layer(state):
         assert compact_fn("blocks.1.attn", q) is None
+        assert not state.attention_output_compact
         writer = compact_fn("blocks.0.attn", q)
+        assert state.attention_output_compact  # the caller learns the output is compact
         assert tuple(writer.output.shape) == (6, 2, 4) and not bool(writer.output.any())
         value = torch.arange(1, 3, dtype=torch.bfloat16).view(2, 1, 1).expand(2, 2, 4)
         writer.write_rows(0, "media", 1, torch.tensor([2, 4]), value)  # global rows 3, 5
