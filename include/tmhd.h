@@ -433,7 +433,8 @@ int tmhd_weight_quant_i8(int8_t *q, float *scale, const void *w, int32_t n,
  * (stride ldb), i.e. the [k][n] column-major operand of cutlass_scaled_mm.
  * Replaces vLLM cutlass_scaled_mm called at
  * src/taomate_hd/inference/w8a8.py:72 and :142-144.
- * k must be a multiple of 64; a, b rows 16-byte aligned.
+ * k must be a multiple of 64 (a multiple of 128 takes the faster
+ * one-wave-per-SIMD kernel); a, b rows 16-byte aligned.
  */
 int tmhd_gemm_w8a8(void *out, const int8_t *a, const int8_t *b,
                    const float *a_scale, const float *b_scale,
@@ -453,7 +454,7 @@ int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m,
  * No counterpart in the reference (the caller-provided scratch of the two
  * GEMMs above).  When the 256 x 256 tiles leave a last round that fills at
  * most half of the CUs (or fill less than half in all), that round's tiles
- * are split along k into up to CUs / tiles parts of at least 4 k-stages;
+ * are split along k into up to CUs / tiles parts of at least 256 bytes of k;
  * the parts' int32 partial tiles go to `workspace` and a second pass adds
  * them (exactly) and applies the same epilogue, so results are bit-identical
  * to the unsplit GEMM.  tmhd_gemm_split_workspace_bytes gives the bytes this
@@ -481,7 +482,7 @@ int tmhd_gemm_i8_i32_ws(int32_t *out, const int8_t *a, const int8_t *b, int32_t 
  * of g, u = the bf16 projection values of tmhd_gemm_w8a8 for gate j and up j,
  * the SwiGLU of tmhd_swiglu: bit-identical to tmhd_gemm_w8a8 then
  * tmhd_swiglu on the de-interleaved projection.  n a multiple of 256, k of
- * 64; out 16-byte aligned rows; same optional split workspace as
+ * 128; out 16-byte aligned rows; same optional split workspace as
  * tmhd_gemm_w8a8_ws.
  */
 int tmhd_gemm_w8a8_swiglu_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,

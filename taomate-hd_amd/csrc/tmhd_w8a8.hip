@@ -346,19 +346,18 @@ gemm_i8_kernel(const GArgs ga) {
 // per lane in AGPRs).  A 32-byte k-step reads 4 A and 4 B operands
 // (ds_read_b128) for 16 MFMAs; the next k-step's reads are issued under the
 // current one's MFMAs, one read per MFMA.
-// k-stages of 64 bytes (two k-steps) cycle through a 5-deep LDS ring (5 x 32
-// KiB, all of the CU's LDS) filled by global_load_lds_dwordx4, four stages
-// ahead.  Stage s has one barrier, after its k-step 0 (whose slots already
-// read k-step 1's operands): behind it, stage s+1 is complete for k-step 1 to
-// prefetch from, and stage s's slot is free for stage s+5, whose loads go out
-// under k-step 1's MFMAs.
-// LDS rows are 64 bytes (4 chunks); chunk c of row r sits at c ^ ((r >> 2) & 3),
-// so the 16 lanes of one ds_read_b128 phase (16 consecutive rows) hit 16
-// distinct 16-byte bank groups.
-constexpr int HBM_ = 256, HBN = 256, HKS = 64, HWAVES = 4, HRING = 5;
-constexpr int HSIDE = HBM_ * HKS;  // bytes of one operand's stage
-constexpr int HSTAGE = 2 * HSIDE;  // A then B
-constexpr int HLOADS = 2 * HSIDE / 1024 / HWAVES;  // 1 KiB wave loads per wave and stage
+// k moves in blocks of 128 bytes (four k-steps).  A block's operands sit in
+// two ring units, one per 128-row half of the tile (rows of 128 bytes: whole
+// cache lines, so each 1 KiB global_load_lds_dwordx4 touches 8 lines and
+// every line is fetched once -- against 16 half-used lines per load with
+// 64-byte rows, which measured 9% slower on the 12,252 x 5,120 x 13,824
+// projection and the 12,252 x 5,376 x 28,672 FC1, with the load path's
+// address unit stalled by the L1 27% of the time).  Units cycle through a
+// 5-deep ring (5 x 32 KiB, all of the CU's LDS), 3 to 7 k-steps ahead of
+// their first read; a 3-deep ring of 64-byte stages (about 4 k-steps ahead)
+// was as fast as the 5-deep one, so the shorter lookahead costs nothing.
+constexpr int HBM_ = 256, HBN = 256, HKD = 128, HWAVES = 4, HRING = 5;
+constexpr int HUNIT = 2 * 128 * HKD;  // bytes of one ring unit: 128 rows of A, then of B
 
 __device__ __forceinline__ void hload_lds16(const void *base, uint32_t off, uint32_t lds_addr) {
   asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
@@ -372,62 +371,65 @@ template <bool RAW, bool SPLIT, bool GLU = false>
 __global__ void __launch_bounds__(HWAVES * 64) __attribute__((amdgpu_waves_per_eu(1, 1)))
 gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma clang fp contract(off)
-  __shared__ __attribute__((aligned(1024))) char smem[HRING * HSTAGE];
+  __shared__ __attribute__((aligned(1024))) char smem[HRING * HUNIT];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
   const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = w >> 1, wn = w & 1;  // wave tile: a rows [wm*128, +128), b rows [wn*128, +128)
-  // whole tile, or (SPLIT) k-stage range [s_begin, s_end) of a tile of the split round
-  const int nst_all = ga.k / HKS;
-  int L, part = 0, s_begin = 0, s_end = nst_all;
+  // whole tile, or (SPLIT) k-block range [d_begin, d_end) of a tile of the split round
+  const int nd_all = ga.k / HKD;
+  int L, part = 0, d_begin = 0, d_end = nd_all;
   if constexpr (SPLIT) {
     const int item = blockIdx.x / ga.nsplit;
     part = blockIdx.x - item * ga.nsplit;
     L = ga.full + item;
-    s_begin = nst_all * part / ga.nsplit;
-    s_end = nst_all * (part + 1) / ga.nsplit;
+    d_begin = nd_all * part / ga.nsplit;
+    d_end = nd_all * (part + 1) / ga.nsplit;
   } else {
     L = xcd_logical_id(blockIdx.x, gridDim.x);
   }
   int tm, tn;
   grouped_tile(L, ga.tm_count, ga.tn_count, tm, tn);
   const int m0 = tm * HBM_, n0 = tn * HBN;
-  const int8_t *abase = ga.a + (int64_t)s_begin * HKS, *bbase = ga.b + (int64_t)s_begin * HKS;
+  const int8_t *abase = ga.a + (int64_t)d_begin * HKD, *bbase = ga.b + (int64_t)d_begin * HKD;
+  const int nd = d_end - d_begin;  // >= 1
 
-  // loads: 16 blocks of 1 KiB (16 rows of 64 B) per operand and stage; wave w
-  // loads blocks w, w + 4, w + 8, w + 12 of each.  Lane: row 16 blk + lane / 4,
-  // physical chunk lane % 4, logical chunk (lane % 4) ^ ((row >> 2) & 3) -- the
-  // same for all of the wave's blocks.
-  const int lch = (lane & 3) ^ ((lane >> 4) & 3);
-  uint32_t aoff[4], boff[4];
+  // Unit u = (k block u / 2, row half u % 2): rows [128 h, 128 h + 128) of the
+  // A and the B tile over 128 bytes of k, in ring slot u % HRING (16 KiB of A,
+  // then 16 KiB of B, rows of 128 bytes).  Chunk c of row r sits at
+  // c ^ ((r >> 1) & 7): the 16 rows of a ds_read_b128 phase cover both row
+  // parities and 8 chunk positions, i.e. all 16 bank groups.
+  // Loads: a unit is 16 blocks of 1 KiB (8 rows x 128 bytes: whole cache
+  // lines) per operand; wave w loads blocks w, w + 4, w + 8, w + 12 of each.
+  // Lane: row 8 blk + lane / 8, physical chunk lane % 8, logical chunk
+  // (lane % 8) ^ ((row >> 1) & 7) -- the same for all of the wave's blocks,
+  // whose parity is w's.
+  const int lch = (lane & 7) ^ ((4 * (w & 1) + (lane >> 4)) & 7);
+  uint32_t aoff[2][4], boff[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = (w + 4 * i) * 16 + (lane >> 2);
-    aoff[i] = (uint32_t)((int64_t)min(m0 + row, ga.m - 1) * ga.lda) + lch * 16;
-    boff[i] = (uint32_t)((int64_t)min(n0 + row, ga.n - 1) * ga.ldb) + lch * 16;
-  }
-  auto load_one = [&](int n, int kt, uint32_t stage) {
-    const int i = n & 3;
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = h * 128 + (w + 4 * i) * 8 + (lane >> 3);
+      aoff[h][i] = (uint32_t)((int64_t)min(m0 + row, ga.m - 1) * ga.lda) + lch * 16;
+      boff[h][i] = (uint32_t)((int64_t)min(n0 + row, ga.n - 1) * ga.ldb) + lch * 16;
+    }
+  // load n (0..7) of unit u: n < 4 A block w + 4 n, else B block w + 4 (n - 4).
+  // Units past the last k block repeat it (in-bounds bytes into a slot nobody reads).
+  auto load_one = [&](int u, int n) {
+    const int j = min(u >> 1, nd - 1), h = u & 1, i = n & 3;
+    const uint32_t dst = lds0 + (uint32_t)((u % HRING) * HUNIT) + (w + 4 * i) * 1024;
     if (n < 4)
-      hload_lds16(abase + (int64_t)kt * HKS, aoff[i], stage + (w + 4 * i) * 1024);
+      hload_lds16(abase + (int64_t)j * HKD, aoff[h][i], dst);
     else
-      hload_lds16(bbase + (int64_t)kt * HKS, boff[i], stage + HSIDE + (w + 4 * i) * 1024);
+      hload_lds16(bbase + (int64_t)j * HKD, boff[h][i], dst + HUNIT / 2);
   };
-  // operand read offsets (k-step ks): row base + swizzled chunk 2 ks + g
-  const int x = (lr >> 2) & 3;
-  uint32_t ard[2], brd[2];
+  // operand read offsets within a unit's operand part, k-step q (0..3) of the
+  // block: row lr (+ 32 per block), logical chunk 2 q + g
+  uint32_t rdq[4];
 #pragma unroll
-  for (int ks = 0; ks < 2; ++ks) {
-    const uint32_t c = (uint32_t)(((2 * ks + g) ^ x) * 16);
-    ard[ks] = (uint32_t)((wm * 128 + lr) * HKS) + c;
-    brd[ks] = (uint32_t)(HSIDE + (wn * 128 + lr) * HKS) + c;
-  }
+  for (int q = 0; q < 4; ++q) rdq[q] = (uint32_t)(lr * HKD + (((2 * q + g) ^ ((lr >> 1) & 7)) * 16));
   auto rd = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
-  // operand r of k-step ks in ring slot sb: r < 4: A block r, else B block r - 4
-  auto read_op = [&](int sb, int ks, int r) -> i32x4 {
-    if (r < 4) return rd(sb * HSTAGE + ard[ks] + r * 32 * HKS);
-    return rd(sb * HSTAGE + brd[ks] + (r - 4) * 32 * HKS);
-  };
 
   i32x16 acc[4][4];  // [n block][m block], D[n][m]
 #pragma unroll
@@ -437,36 +439,42 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int nst = s_end - s_begin;  // >= 1
-  // prologue: stages 0..4 in flight (past the last stage the loads repeat it,
-  // into slots that are never read); stage 0 landed, then its k-step 0 operands
+  // prologue: units 0..3 in flight; units 0 and 1 (k block 0) landed
 #pragma unroll
-  for (int st = 0; st < HRING; ++st)
+  for (int u = 0; u < 4; ++u)
 #pragma unroll
-    for (int n = 0; n < HLOADS; ++n) load_one(n, min(st, nst - 1), lds0 + st * HSTAGE);
-  constexpr int VW0 = (HRING - 1) * HLOADS, VW1 = (HRING - 2) * HLOADS;  // loads that may stay in flight
-  static_assert(VW0 < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | (VW0 & 15) | ((VW0 >> 4) << 14));
+    for (int n = 0; n < 8; ++n) load_one(u, n);
+  __builtin_amdgcn_s_waitcnt(0x0f70 | 16);  // vmcnt(16): units 2, 3 may stay in flight
   __syncthreads();
   i32x4 cur[8], nxt[8];
+  // operand r of k-step q of k block d (ring position dm = d % HRING): r < 4
+  // A block r from unit 2 d + wm, else B block r - 4 from unit 2 d + wn
+  auto read_op = [&](int dm, int q, int r) -> i32x4 {
+    if (r < 4) return rd((uint32_t)(((2 * dm + wm) % HRING) * HUNIT) + rdq[q] + r * 32 * HKD);
+    return rd((uint32_t)(((2 * dm + wn) % HRING) * HUNIT + HUNIT / 2) + rdq[q] + (r - 4) * 32 * HKD);
+  };
 #pragma unroll
   for (int r = 0; r < 8; ++r) cur[r] = read_op(0, 0, r);
 
-  // one stage in ring slot sb: k-steps 0 and 1; stage s + 1 is in slot (sb + 1) % HRING
-  auto stage = [&](auto sb_c, int s) {
-    constexpr int sb = decltype(sb_c)::value, sn = (sb + 1) % HRING;
+  // k block d at ring position dm: k-steps 0..3.  Unit 2 d + 4 is loaded under
+  // k-step 0 and unit 2 d + 5 under k-step 3, one load per two MFMAs.  One
+  // barrier, in front of k-step 3: behind it, units 2 d + 2 and 2 d + 3 (block
+  // d + 1) have landed for k-step 3 to read ahead from, and nobody reads
+  // block d's units any more (k-step 3's operands are already in registers),
+  // so their slots take units 2 d + 5 and 2 d + 6.
+  auto block = [&](auto dm_c, int d) {
+    constexpr int dm = decltype(dm_c)::value, dn = (dm + 1) % HRING;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 1) {
-        // stage s + 1 landed (stages s + 2 .. s + HRING - 1 may stay in
-        // flight) and visible; slot sb free for stage s + HRING
-        __builtin_amdgcn_s_waitcnt(0x0f70 | (VW1 & 15) | ((VW1 >> 4) << 14));
+    for (int q = 0; q < 4; ++q) {
+      if (q == 3) {
+        __builtin_amdgcn_s_waitcnt(0x0f70 | 8);  // vmcnt(8): unit 2 d + 4 may stay in flight
         __syncthreads();
       }
 #pragma unroll
       for (int idx = 0; idx < 16; ++idx) {
-        if (idx < 8) nxt[idx] = ks == 0 ? read_op(sb, 1, idx) : read_op(sn, 0, idx);
-        if (ks == 1 && idx % 2 == 0) load_one(idx / 2, min(s + HRING, nst - 1), lds0 + sb * HSTAGE);
+        if (idx < 8) nxt[idx] = q < 3 ? read_op(dm, q + 1, idx) : read_op(dn, 0, idx);
+        if (q == 0 && idx % 2 == 0) load_one(2 * d + 4, idx / 2);
+        if (q == 3 && idx % 2 == 0) load_one(2 * d + 5, idx / 2);
         const int nb = idx >> 2, mb = idx & 3;
         acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[4 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
@@ -475,18 +483,18 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       for (int r = 0; r < 8; ++r) cur[r] = nxt[r];
     }
   };
-  int s = 0;
-  for (; s + HRING <= nst; s += HRING) {
-    stage(std::integral_constant<int, 0>{}, s);
-    stage(std::integral_constant<int, 1>{}, s + 1);
-    stage(std::integral_constant<int, 2>{}, s + 2);
-    stage(std::integral_constant<int, 3>{}, s + 3);
-    stage(std::integral_constant<int, 4>{}, s + 4);
+  int d = 0;
+  for (; d + HRING <= nd; d += HRING) {
+    block(std::integral_constant<int, 0>{}, d);
+    block(std::integral_constant<int, 1>{}, d + 1);
+    block(std::integral_constant<int, 2>{}, d + 2);
+    block(std::integral_constant<int, 3>{}, d + 3);
+    block(std::integral_constant<int, 4>{}, d + 4);
   }
-  if (s < nst) stage(std::integral_constant<int, 0>{}, s);
-  if (s + 1 < nst) stage(std::integral_constant<int, 1>{}, s + 1);
-  if (s + 2 < nst) stage(std::integral_constant<int, 2>{}, s + 2);
-  if (s + 3 < nst) stage(std::integral_constant<int, 3>{}, s + 3);
+  if (d < nd) block(std::integral_constant<int, 0>{}, d);
+  if (d + 1 < nd) block(std::integral_constant<int, 1>{}, d + 1);
+  if (d + 2 < nd) block(std::integral_constant<int, 2>{}, d + 2);
+  if (d + 3 < nd) block(std::integral_constant<int, 3>{}, d + 3);
   // every wave drains its loads before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0x0f70);
 
@@ -538,7 +546,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       // bf16 tile through LDS: each wave stages its 128 x 128 outputs in rows
       // of 256 + 16 bytes, then writes 16 bytes per lane, 256-byte row segments
       constexpr int ROWB = 128 * 2 + 16;
-      static_assert(HWAVES * 128 * ROWB <= HRING * HSTAGE, "staging fits the ring");
+      static_assert(HWAVES * 128 * ROWB <= HRING * HUNIT, "staging fits the ring");
       __syncthreads();  // every wave is done with the ring
       const uint32_t wt = (uint32_t)(w * 128 * ROWB);
 #pragma unroll
@@ -725,17 +733,17 @@ __global__ void __launch_bounds__(256) gemm_split_merge_kernel(const GArgs ga) {
 }
 
 // K split of the last, partial round of 256 x 256 tiles (all tiles when they
-// fill less than half the CUs): its tiles' k-stages are dealt to S parts, S
-// up to CUs / tiles and at least 4 stages per part, so that the round fills
-// the CUs; the partials are merged by gemm_split_merge_kernel.
+// fill less than half the CUs): its tiles' 128-byte k blocks are dealt to S
+// parts, S up to CUs / tiles and at least 2 blocks per part, so that the
+// round fills the CUs; the partials are merged by gemm_split_merge_kernel.
 void gemm_split_plan(int32_t m, int32_t n, int32_t k, int &tail, int &parts) {
   tail = 0, parts = 1;
   const int cus = device_cus();
-  if (cus <= 0 || m <= 0 || n <= 0 || k <= 0 || k % HKS) return;
+  if (cus <= 0 || m <= 0 || n <= 0 || k <= 0 || k % HKD) return;
   const int64_t tiles = (int64_t)((m + HBM_ - 1) / HBM_) * ((n + HBN - 1) / HBN);
   const int64_t t = tiles % cus;
   if (t == 0 || 2 * t > cus) return;
-  const int64_t s = std::min<int64_t>(cus / t, (k / HKS) / 4);
+  const int64_t s = std::min<int64_t>(cus / t, (k / HKD) / 2);
   if (s < 2) return;
   tail = (int)t, parts = (int)s;
 }
@@ -758,10 +766,11 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
            (int32_t)(((uintptr_t)bs % 16) == 0 && ((uintptr_t)bias % 8) == 0),
            (int32_t)(!RAW && ((uintptr_t)out % 16) == 0 && ldo % 8 == 0), (int32_t)tiles, 1, nullptr};
   const int64_t grid = tiles;
-  // the one-wave-per-SIMD kernel takes 32-bit row offsets
+  // the one-wave-per-SIMD kernel takes 32-bit row offsets and whole 128-byte
+  // k blocks; other shapes (k an odd multiple of 64) run the 8-wave kernel
   const bool wide = (int64_t)(m - 1) * lda + k < ((int64_t)1 << 32) &&
                     (int64_t)(n - 1) * ldb + k < ((int64_t)1 << 32);
-  if (wide) {
+  if (wide && k % HKD == 0) {
     int tail = 0, parts = 1;
     gemm_split_plan(m, n, k, tail, parts);
     if (parts > 1 && ws && ((uintptr_t)ws % 16) == 0 && ws_bytes >= gemm_split_bytes(tail, parts)) {
@@ -791,9 +800,9 @@ int launch_gemm_glu(void *out, const int8_t *a, const int8_t *b, const float *as
                     int64_t ws_bytes, void *stream) {
   const char *what = "tmhd_gemm_w8a8_swiglu_ws";
   if (m < 0 || n <= 0 || k <= 0) return set_error(TMHD_ERR_INVALID, "%s: m %d n %d k %d", what, m, n, k);
-  if (k % HKS || n % 256)
+  if (k % HKD || n % 256)
     return set_error(TMHD_ERR_UNSUPPORTED, "%s: k %d (a multiple of %d), n %d (gate + up, a multiple of 256)", what,
-                     k, HKS, n);
+                     k, HKD, n);
   if (!out || !a || !b || !as || !bs) return set_error(TMHD_ERR_INVALID, "%s: null pointer", what);
   if (((uintptr_t)a % 16) || ((uintptr_t)b % 16) || lda % 16 || ldb % 16 || lda < k || ldb < k || ldo < n / 2 ||
       ((uintptr_t)out % 16) || ldo % 8)

@@ -70,6 +70,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
         _native.check(lib.tmhd_attn_fwd_bf16(args, None), "attn")
     with pytest.raises(ValueError, match="multiple of 64"):
         _native.check(lib.tmhd_gemm_i8_i32(None, None, None, 4, 4, 100, 100, 100, 4, None), "gemm")
+    # the SwiGLU GEMM exists only in the kernel with 128-byte k blocks
+    with pytest.raises(ValueError, match="multiple of 128"):
+        _native.check(lib.tmhd_gemm_w8a8_swiglu_ws(None, None, None, None, None, None, 4, 256, 192, 192, 192, 128,
+                                                   None, 0, None), "swiglu gemm")
     with pytest.raises(ValueError, match="cols"):
         _native.check(lib.tmhd_token_quant_i8(None, None, None, 4, 12, 12, None), "quant")
 

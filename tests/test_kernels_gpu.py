@@ -234,7 +234,11 @@ def test_weight_quant_bit_exact(torch_mod, dev):
     assert np.array_equal(s.cpu().numpy().reshape(-1), wsc)
 
 
-@pytest.mark.parametrize("m,n,k", [(12, 32, 64), (300, 520, 1024), (513, 256, 5120)])
+# k = 64 and 192 (odd multiples of 64) run the 8-wave kernel; 128 (one k block:
+# the ring's tail alone), 640 (one whole pass of the 5-unit ring), 1024 and
+# 5120 the one-wave-per-SIMD kernel
+@pytest.mark.parametrize("m,n,k", [(12, 32, 64), (257, 300, 192), (130, 260, 128), (64, 512, 640), (300, 520, 1024),
+                                   (513, 256, 5120)])
 def test_gemm_accumulators_and_epilogue_bit_exact(torch_mod, dev, m, n, k):
     torch = torch_mod
     from taomate_hd_amd import quant
