@@ -16,6 +16,10 @@ row ops around the call (Q/K norm + RoPE, RMSNorm / AdaLN / residual gate),
 the Ulysses send layouts, dense packed attention and the CPU baselines of the
 BF16, INT8-QK and W8A8 paths on the host cores.
 
+Every leg is timed at the card's settled clock: the headline BF16 step runs
+W untimed steps first (default 20, about 160 ms), the other legs their W
+steps and then more until SETTLE_MS of their own work has run.
+
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                     [--workload all|bf16|c2|i8qk|w8a8|rope|adaln|packed|mlp|prep|faithful|ulysses|copy]
                     [--no-cpu-baseline] [--no-reference-gpu]
@@ -119,10 +123,34 @@ def hook_step(hook, inputs, cu):
     )
 
 
-def time_steps(torch, fn, steps, warmup):
+# Untimed work each leg runs before its timed steps, besides its warm-up steps:
+# after an idle spell the card boosts, overshoots its power limit and clocks
+# down for a few tens of milliseconds before it settles (the W8A8 GEMM's first
+# calls ran 683 -> 868 -> 680 us, the attention call 9.6 -> 7.9 ms), and a
+# serving loop runs at the settled clock.
+SETTLE_MS = 150.0
+
+
+def settle(torch, fn, settle_ms):
+    """Untimed calls of fn until at least settle_ms of its work has run back to back."""
+    if settle_ms <= 0:
+        return
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    once_ms = max((time.perf_counter() - t0) * 1e3, 1e-3)
+    for _ in range(int(settle_ms / once_ms)):
+        fn()
+    torch.cuda.synchronize()
+
+
+def time_steps(torch, fn, steps, warmup, settle_ms=SETTLE_MS):
+    """Device ms per step over `steps` timed calls of fn, after `warmup` calls
+    and the settle() calls.  Returns (wall ms per step, device ms per step)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    settle(torch, fn, settle_ms)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
@@ -135,7 +163,7 @@ def time_steps(torch, fn, steps, warmup):
     return wall_ms, start.elapsed_time(end) / steps
 
 
-def bench_attention(torch, dev, backend, steps, warmup, cache, inputs):
+def bench_attention(torch, dev, backend, steps, warmup, cache, inputs, settle_ms=SETTLE_MS):
     from taomate_hd_amd import HookMode, StreamingAttentionHook
     from taomate_hd_amd.profiling import ComponentTimer
 
@@ -151,8 +179,9 @@ def bench_attention(torch, dev, backend, steps, warmup, cache, inputs):
 
     for _ in range(warmup):
         step()
+    settle(torch, step, settle_ms)
     timer.reset()
-    wall_ms, dev_ms = time_steps(torch, step, steps, 0)
+    wall_ms, dev_ms = time_steps(torch, step, steps, 0, 0)
     comps = timer.summary()
     hook.deactivate()
     if not bool(torch.isfinite(out).all()):
@@ -523,7 +552,9 @@ def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=20,
+                    help="untimed steps before the timed ones (the headline leg runs exactly these; the other "
+                         "legs also run on until %d ms of their work has run)" % SETTLE_MS)
     ap.add_argument("--no-reference-gpu", action="store_true",
                     help="skip timing the reference's SDPA backend on the GPU beside the bf16 workload")
     ap.add_argument("--workload", choices=("all", "bf16", "c2", "i8qk", "w8a8", "rope", "adaln", "packed", "mlp", "prep",
@@ -594,7 +625,8 @@ def main() -> int:
         cache, inputs = build_stream(torch, dev, None)
         torch.cuda.synchronize()
     if args.workload in ("all", "bf16"):
-        wall_ms, dev_ms, comps = bench_attention(torch, dev, "sdpa", args.steps, args.warmup, cache, inputs)
+        # the headline leg: exactly args.warmup untimed steps, then the timed ones
+        wall_ms, dev_ms, comps = bench_attention(torch, dev, "sdpa", args.steps, args.warmup, cache, inputs, 0)
         attn_ms = comps["attention"]["mean_ms"]
         achieved = ATTN_FLOPS / (attn_ms * 1e-3) / 1e12
         result["value"] = round(ATTN_FLOPS / (wall_ms * 1e-3) / 1e12, 2)
