@@ -549,33 +549,49 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       static_assert(HWAVES * 128 * ROWB <= HRING * HUNIT, "staging fits the ring");
       __syncthreads();  // every wave is done with the ring
       const uint32_t wt = (uint32_t)(w * 128 * ROWB);
+      float asv[4];  // row scales of the lane's 4 m-blocks
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int m = m0 + wm * 128 + j * 32 + lr;
-        const float asm_ = ga.as[min(m, ga.m - 1)];
+      for (int j = 0; j < 4; ++j) asv[j] = ga.as[min(m0 + wm * 128 + j * 32 + lr, ga.m - 1)];
+      // n-blocks outermost, so that one block's column scales and converted
+      // bias are live at a time, and the bias test outside the element loops
+      // (per element: convert, two multiplies, the bias add, half a pack)
+      auto stage_tile = [&](auto has_bias) {
+        constexpr bool HB = decltype(has_bias)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i) {
+          float bf[4][4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            uint16_t vals[4];
-            float tv[4];
+          for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float t = (float)acc[i][j][4 * u + e];
-              t = t * bsv[i][u][e];
-              t = t * asm_;
-              if (ga.bias) {
-                const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
-                t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
-              }
-              tv[e] = t;
+              const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
+              bf[u][e] = HB ? bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu)) : 0.0f;
             }
-            bf16_quad(tv, vals);
-            *(i32x2 *)(smem + wt + (j * 32 + lr) * ROWB + (i * 32 + 8 * u + 4 * g) * 2) =
-                i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
-                      (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
-          }
-      }
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+              uint16_t vals[4];
+              float tv[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float t = (float)acc[i][j][4 * u + e];
+                t = t * bsv[i][u][e];
+                t = t * asv[j];
+                if constexpr (HB) t = t + bf[u][e];
+                tv[e] = t;
+              }
+              bf16_quad(tv, vals);
+              *(i32x2 *)(smem + wt + (j * 32 + lr) * ROWB + (i * 32 + 8 * u + 4 * g) * 2) =
+                  i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                        (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+            }
+        }
+      };
+      if (ga.bias)
+        stage_tile(std::true_type{});
+      else
+        stage_tile(std::false_type{});
       if constexpr (GLU) {
         // gate halves sit in the staging rows of waves (wm, 0), up halves in
         // (wm, 1); each wave writes 64 of the tile's 256 output rows
