@@ -162,6 +162,34 @@ def test_i8qk_attention(torch_mod, dev, heads, dim, lq, splits):
     assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
 
 
+def test_gemm_beyond_32bit_row_offsets(torch_mod, dev):
+    # a [m, k] activation of 4.3 GB: rows 524,288 and later start past 2^32 bytes,
+    # so the GEMM takes the kernel with 64-bit row addressing; sampled rows on
+    # both sides of the boundary are bit-exact (accumulators and epilogue)
+    torch = torch_mod
+    from taomate_hd_amd import quant
+
+    m, n, k = 524288 + 64, 40, 8192
+    g = torch.Generator(device=dev).manual_seed(9)
+    ad = torch.randint(-128, 128, (m, k), dtype=torch.int8, device=dev, generator=g)
+    wd = torch.randint(-127, 128, (n, k), dtype=torch.int8, device=dev, generator=g)
+    sa = torch.rand((m, 1), device=dev, generator=g) * 0.05 + 1e-3
+    sb = torch.rand((1, n), device=dev, generator=g) * 0.01 + 1e-4
+    acc = quant.int8_mm_i32(ad, wd.t())
+    out = quant.cutlass_scaled_mm(ad, wd.t(), sa, sb, torch.bfloat16)
+    torch.cuda.synchronize()
+    rows = torch.tensor(list(range(0, 16)) + list(range(524288 - 16, m)), device=dev)
+    a = ad.index_select(0, rows).cpu().numpy()
+    w = wd.cpu().numpy()
+    want = oq.int_gemm(a, w)
+    assert np.array_equal(acc.index_select(0, rows).cpu().numpy(), want)
+    got = bf16.from_torch(out.index_select(0, rows))
+    assert np.array_equal(got, oq.scaled_mm_epilogue(want, sa.index_select(0, rows).cpu().numpy().ravel(),
+                                                      sb.cpu().numpy().ravel(), None))
+    del ad, acc, out
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("backend", ["bf16", "i8qk"])
 @pytest.mark.parametrize(
     "heads,dim,lq,splits",
