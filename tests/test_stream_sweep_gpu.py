@@ -1,0 +1,117 @@
+"""Seeded random streams through the hook and the in-place cache against the
+oracle's restatement of the reference hook and cache: random head counts and
+head dims, one or two layers, 3-5 blocks, 1-3 documents per call (empty ones
+among them) with the live document at a random place, interleaved commit
+masks with video / audio tags, noisy and clean-commit steps, a random number
+of recent blocks retained after each commit, both backends."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import attention as oatt
+from oracle import bf16
+from oracle import stream as ost
+from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
+
+pytestmark = pytest.mark.gpu
+
+N_STREAMS = 8
+
+
+def _layout(rng: np.random.Generator):
+    """(tags, commit mask, document bounds) of one call: one live document
+    between 0-2 others, its media rows interleaved with condition rows."""
+    ndoc = int(rng.integers(1, 4))
+    live = int(rng.integers(0, ndoc))
+    tags, mask, bounds = [], [], [0]
+    for d in range(ndoc):
+        if d == live:
+            n = int(rng.integers(20, 260))
+            m = rng.random(n) < rng.uniform(0.3, 0.9)
+            m[rng.choice(n, 2, replace=False)] = True  # at least two media rows
+            t = np.where(rng.random(n) < 0.8, 0, 2)  # media: video 0 / audio 2
+            media = np.nonzero(m)[0]
+            t[media[0]], t[media[-1]] = 0, 2  # a commit holds video and audio rows (cache.py contract)
+            t[~m] = np.where(rng.random(int((~m).sum())) < 0.5, 1, 0)  # condition: text 1 / cond 0
+        else:
+            n = int(rng.integers(0, 60))
+            m = np.zeros(n, bool)
+            t = np.where(rng.random(n) < 0.5, 1, -1)
+        tags.append(t.astype(np.int64))
+        mask.append(m)
+        bounds.append(bounds[-1] + n)
+    return np.concatenate(tags), np.concatenate(mask), tuple(bounds)
+
+
+STREAMS = [dict(seed=31000 + 97 * s, backend=("sdpa", "sage_attn")[s % 2]) for s in range(N_STREAMS)]
+
+
+@pytest.mark.parametrize("stream", STREAMS, ids=[f"{s['backend']}-{s['seed']}" for s in STREAMS])
+def test_random_stream_matches_oracle(torch_mod, dev, stream):
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd.hook import HookMode
+
+    rng = np.random.default_rng(stream["seed"])
+    backend = stream["backend"]
+    heads, dim = int(rng.integers(1, 4)), int(rng.choice([64, 128]))
+    layers = ("blocks.0.attn", "blocks.1.attn")[: int(rng.integers(1, 3))]
+    cache = HeadMajorRingKVCache(KVContract(layer_names=layers, local_heads=heads, head_dim=dim))
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
+    ocache, exact_cache = ost.CacheOracle(layers), ost.CacheOracle(layers)
+    ohook, exact_hook = ost.HookOracle(ocache, backend=backend), ost.HookOracle(exact_cache)
+
+    class Attn:
+        softmax_scale = dim ** -0.5
+
+    seed = stream["seed"]
+    for block in range(int(rng.integers(3, 6))):
+        tags, mask, bounds = _layout(rng)
+        total = len(tags)
+        for mode in ("noisy", "clean_commit"):
+            if mode == "clean_commit":
+                for c in (cache, ocache, exact_cache):
+                    c.begin_clean_commit(block)
+            hook.activate(mode=HookMode(mode), block_index=block)
+            ohook.activate(mode, block)
+            exact_hook.activate(mode, block)
+            for layer in layers:
+                seed += 10
+                q = randn_bf16((total, heads, dim), seed)
+                k = randn_bf16((total, heads, dim), seed + 1, offset=key_offset(heads, dim, seed + 2))
+                v = randn_bf16((total, heads, dim), seed + 3)
+                out = hook(
+                    attention=Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
+                    value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
+                    commit_mask=torch.tensor(mask, device=dev),
+                    cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=bounds,
+                    max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])),
+                )
+                torch.cuda.synchronize()
+                got = bf16.from_torch(out)
+                want = ohook(layer, q, k, v, tags, mask, bounds, dim ** -0.5)
+                exact = exact_hook(layer, q, k, v, tags, mask, bounds, dim ** -0.5)
+                if backend == "sdpa":
+                    mx, mean = err_stats(got, want)
+                    # few-key documents give O(1) outputs whose bf16 rounding alone nears 1e-3
+                    mean_round = float(np.abs(bf16.round_f32(want.astype(np.float32)) - want).mean())
+                    assert mx <= 2e-2 and mean <= max(1e-3, 1.5 * mean_round), (block, mode, layer, mx, mean)
+                else:
+                    assert oatt.cosine(got, exact) >= 0.999, (block, mode, layer)
+            hook.deactivate()
+            ohook.deactivate()
+            exact_hook.deactivate()
+        for c in (cache, ocache, exact_cache):
+            c.commit()
+        keep = int(rng.integers(1, 3))
+        for c in (cache, ocache, exact_cache):
+            c.retain_sink_and_recent_commits(keep)
+        assert list(cache.commit_token_counts) == ocache.counts
+        assert list(cache.commit_token_tags) == ocache.tags
+        for layer in layers:
+            pair = cache.history(layer)
+            want_k, want_v = ocache.history(layer)
+            assert np.array_equal(bf16.from_torch(pair.key), want_k)
+            assert np.array_equal(bf16.from_torch(pair.value), want_v)
