@@ -2,8 +2,9 @@
 oracle's restatement of the reference hook and cache: random head counts and
 head dims, one or two layers, 3-5 blocks, 1-3 documents per call (empty ones
 among them) with the live document at a random place, interleaved commit
-masks with video / audio tags, noisy and clean-commit steps, a random number
-of recent blocks retained after each commit, both backends."""
+masks with video / audio tags, noisy and clean-commit steps, 0-2 recent
+blocks retained after each commit with the sink video-only or whole, both
+backends."""
 
 from __future__ import annotations
 
@@ -105,9 +106,9 @@ def test_random_stream_matches_oracle(torch_mod, dev, stream):
             exact_hook.deactivate()
         for c in (cache, ocache, exact_cache):
             c.commit()
-        keep = int(rng.integers(1, 3))
+        keep, video_only = int(rng.integers(0, 3)), bool(rng.integers(0, 2))
         for c in (cache, ocache, exact_cache):
-            c.retain_sink_and_recent_commits(keep)
+            c.retain_sink_and_recent_commits(keep, sink_video_only=video_only)
         assert list(cache.commit_token_counts) == ocache.counts
         assert list(cache.commit_token_tags) == ocache.tags
         for layer in layers:
