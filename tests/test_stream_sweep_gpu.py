@@ -2,7 +2,8 @@
 oracle's restatement of the reference hook and cache: random head counts and
 head dims, one or two layers, 3-5 blocks, 1-3 documents per call (empty ones
 among them) with the live document at a random place, interleaved commit
-masks with video / audio tags, noisy and clean-commit steps, 0-2 recent
+masks with video / audio tags, noisy steps, commits through clean-commit or
+fused progress-denoise steps (random sink / recent views), 0-2 recent
 blocks retained after each commit with the sink video-only or whole, both
 backends."""
 
@@ -22,8 +23,9 @@ N_STREAMS = 8
 
 
 def _layout(rng: np.random.Generator):
-    """(tags, commit mask, document bounds) of one call: one live document
-    between 0-2 others, its media rows interleaved with condition rows."""
+    """(tags, commit mask, document bounds, live document) of one call: one
+    live document between 0-2 others, its media rows interleaved with
+    condition rows."""
     ndoc = int(rng.integers(1, 4))
     live = int(rng.integers(0, ndoc))
     tags, mask, bounds = [], [], [0]
@@ -43,7 +45,7 @@ def _layout(rng: np.random.Generator):
         tags.append(t.astype(np.int64))
         mask.append(m)
         bounds.append(bounds[-1] + n)
-    return np.concatenate(tags), np.concatenate(mask), tuple(bounds)
+    return np.concatenate(tags), np.concatenate(mask), tuple(bounds), live
 
 
 STREAMS = [dict(seed=31000 + 97 * s, backend=("sdpa", "sage_attn")[s % 2]) for s in range(N_STREAMS)]
@@ -68,42 +70,58 @@ def test_random_stream_matches_oracle(torch_mod, dev, stream):
         softmax_scale = dim ** -0.5
 
     seed = stream["seed"]
-    for block in range(int(rng.integers(3, 6))):
-        tags, mask, bounds = _layout(rng)
+
+    def step(mode, block, tags, mask, bounds, hint=None, **kw):
+        nonlocal seed
         total = len(tags)
-        for mode in ("noisy", "clean_commit"):
-            if mode == "clean_commit":
-                for c in (cache, ocache, exact_cache):
-                    c.begin_clean_commit(block)
-            hook.activate(mode=HookMode(mode), block_index=block)
-            ohook.activate(mode, block)
-            exact_hook.activate(mode, block)
-            for layer in layers:
-                seed += 10
-                q = randn_bf16((total, heads, dim), seed)
-                k = randn_bf16((total, heads, dim), seed + 1, offset=key_offset(heads, dim, seed + 2))
-                v = randn_bf16((total, heads, dim), seed + 3)
-                out = hook(
-                    attention=Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
-                    value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
-                    commit_mask=torch.tensor(mask, device=dev),
-                    cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=bounds,
-                    max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])),
-                )
-                torch.cuda.synchronize()
-                got = bf16.from_torch(out)
-                want = ohook(layer, q, k, v, tags, mask, bounds, dim ** -0.5)
-                exact = exact_hook(layer, q, k, v, tags, mask, bounds, dim ** -0.5)
-                if backend == "sdpa":
-                    mx, mean = err_stats(got, want)
-                    # few-key documents give O(1) outputs whose bf16 rounding alone nears 1e-3
-                    mean_round = float(np.abs(bf16.round_f32(want.astype(np.float32)) - want).mean())
-                    assert mx <= 2e-2 and mean <= max(1e-3, 1.5 * mean_round), (block, mode, layer, mx, mean)
-                else:
-                    assert oatt.cosine(got, exact) >= 0.999, (block, mode, layer)
-            hook.deactivate()
-            ohook.deactivate()
-            exact_hook.deactivate()
+        hook.activate(mode=HookMode(mode), block_index=block, **kw)
+        for o in (ohook, exact_hook):
+            o.activate(mode, block, kw.get("fused_current_use_sink"), kw.get("fused_current_recent_blocks"))
+        for layer in layers:
+            seed += 10
+            q = randn_bf16((total, heads, dim), seed)
+            k = randn_bf16((total, heads, dim), seed + 1, offset=key_offset(heads, dim, seed + 2))
+            v = randn_bf16((total, heads, dim), seed + 3)
+            out = hook(
+                attention=Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
+                value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
+                commit_mask=torch.tensor(mask, device=dev),
+                cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=bounds,
+                max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])), live_documents_hint=hint,
+            )
+            torch.cuda.synchronize()
+            got = bf16.from_torch(out)
+            want = ohook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint)
+            exact = exact_hook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint)
+            if backend == "sdpa":
+                mx, mean = err_stats(got, want)
+                # few-key documents give O(1) outputs whose bf16 rounding alone nears 1e-3
+                mean_round = float(np.abs(bf16.round_f32(want.astype(np.float32)) - want).mean())
+                assert mx <= 2e-2 and mean <= max(1e-3, 1.5 * mean_round), (block, mode, layer, mx, mean)
+            else:
+                assert oatt.cosine(got, exact) >= 0.999, (block, mode, layer)
+        hook.deactivate()
+        ohook.deactivate()
+        exact_hook.deactivate()
+
+    for block in range(int(rng.integers(3, 6))):
+        tags, mask, bounds, live = _layout(rng)
+        step("noisy", block, tags, mask, bounds)
+        for c in (cache, ocache, exact_cache):
+            c.begin_clean_commit(block)
+        if rng.random() < 0.5:
+            step("clean_commit", block, tags, mask, bounds)
+        else:
+            # the block's media committed by a fused step: its document, then the next chunk's
+            tags2, mask2, bounds2, live2 = _layout(rng)
+            ftags, fmask = np.concatenate([tags, tags2]), np.concatenate([mask, mask2])
+            fbounds = (*bounds, *(len(tags) + b for b in bounds2[1:]))
+            kw = {}
+            if rng.random() < 0.7:
+                kw = dict(fused_current_use_sink=bool(rng.integers(0, 2)),
+                          fused_current_recent_blocks=int(rng.integers(1, 4)))
+            step("fused_progress_denoise", block, ftags, fmask, fbounds,
+                 hint=(live, len(bounds) - 1 + live2), **kw)
         for c in (cache, ocache, exact_cache):
             c.commit()
         keep, video_only = int(rng.integers(0, 3)), bool(rng.integers(0, 2))
