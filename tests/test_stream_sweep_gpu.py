@@ -4,7 +4,8 @@ head dims, one or two layers, 3-5 blocks, 1-3 documents per call (empty ones
 among them) with the live document at a random place, interleaved commit
 masks with video / audio tags, noisy steps, commits through clean-commit or
 fused progress-denoise steps (random sink / recent views), 0-2 recent
-blocks retained after each commit with the sink video-only or whole, both
+blocks retained after each commit with the sink video-only or whole, random
+condition-cache decisions (cached documents, compact output rows), both
 backends."""
 
 from __future__ import annotations
@@ -54,7 +55,7 @@ STREAMS = [dict(seed=31000 + 97 * s, backend=("sdpa", "sage_attn")[s % 2]) for s
 @pytest.mark.parametrize("stream", STREAMS, ids=[f"{s['backend']}-{s['seed']}" for s in STREAMS])
 def test_random_stream_matches_oracle(torch_mod, dev, stream):
     torch = torch_mod
-    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook, condition
     from taomate_hd_amd.hook import HookMode
 
     rng = np.random.default_rng(stream["seed"])
@@ -71,9 +72,28 @@ def test_random_stream_matches_oracle(torch_mod, dev, stream):
 
     seed = stream["seed"]
 
+    def decisions(tags, mask, bounds, live_docs):
+        """Random condition-cache decisions for one call: cached live documents
+        (their condition rows are skipped) and, or not, a compact row order
+        that drops those rows and random rows of the other documents."""
+        if rng.random() >= 0.35:
+            return (), None
+        cached = tuple(d for d in live_docs if rng.random() < 0.6)
+        if rng.random() < 0.5:
+            return cached, None
+        keep = np.ones(len(tags), bool)
+        for d, (a, b) in enumerate(zip(bounds, bounds[1:])):
+            if d in cached:
+                keep[a:b] &= mask[a:b]  # its condition rows leave the compact order
+            elif d not in live_docs:
+                keep[a:b] &= rng.random(b - a) < 0.7  # rows of other documents may be dropped
+        return cached, [int(r) for r in np.nonzero(keep)[0]]
+
     def step(mode, block, tags, mask, bounds, hint=None, **kw):
         nonlocal seed
         total = len(tags)
+        live_docs = hint if hint is not None else tuple(
+            d for d, (a, b) in enumerate(zip(bounds, bounds[1:])) if mask[a:b].any())
         hook.activate(mode=HookMode(mode), block_index=block, **kw)
         for o in (ohook, exact_hook):
             o.activate(mode, block, kw.get("fused_current_use_sink"), kw.get("fused_current_recent_blocks"))
@@ -82,17 +102,22 @@ def test_random_stream_matches_oracle(torch_mod, dev, stream):
             q = randn_bf16((total, heads, dim), seed)
             k = randn_bf16((total, heads, dim), seed + 1, offset=key_offset(heads, dim, seed + 2))
             v = randn_bf16((total, heads, dim), seed + 3)
-            out = hook(
-                attention=Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
-                value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
-                commit_mask=torch.tensor(mask, device=dev),
-                cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=bounds,
-                max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])), live_documents_hint=hint,
-            )
+            cached, kept = decisions(tags, mask, bounds, live_docs)
+            state = condition.ConditionLayerState(layer, cached_documents=cached, compact_rows=kept)
+            with condition.condition_layer(state):
+                out = hook(
+                    attention=Attn(), layer_name=layer, query=to_dev(q, dev), key=to_dev(k, dev),
+                    value=to_dev(v, dev), token_tags=torch.tensor(tags, device=dev),
+                    commit_mask=torch.tensor(mask, device=dev),
+                    cu_seqlens=torch.tensor(bounds, dtype=torch.int32, device=dev), cu_seqlens_host=bounds,
+                    max_seqlen=max(b - a for a, b in zip(bounds, bounds[1:])), live_documents_hint=hint,
+                )
             torch.cuda.synchronize()
             got = bf16.from_torch(out)
-            want = ohook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint)
-            exact = exact_hook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint)
+            kwc = {"cached_documents": cached, "compact_rows": kept}
+            want = ohook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint, **kwc)
+            exact = exact_hook(layer, q, k, v, tags, mask, bounds, dim ** -0.5, live_documents_hint=hint, **kwc)
+            assert got.shape == want.shape and state.attention_output_compact == (kept is not None)
             if backend == "sdpa":
                 mx, mean = err_stats(got, want)
                 # few-key documents give O(1) outputs whose bf16 rounding alone nears 1e-3
