@@ -377,8 +377,9 @@ def bench_adaln(torch, dev, steps, warmup):
     """The DiT block's row ops around one attention call on the 768p chunk's
     hidden rows (LQ x 5376, bf16, AdaLN tables as strided chunks of one
     projection): pre-attention RMSNorm + modulate and post-attention residual
-    gate + RMSNorm + modulate.  Returns {name: (ms per call, bytes per call)}."""
-    from taomate_hd_amd import fused_residual_gate_rms_norm_modulate, fused_rms_norm_modulate
+    gate + RMSNorm + modulate, alone and followed by the next projection's
+    token quant of its output.  Returns {name: (ms per call, bytes per call)}."""
+    from taomate_hd_amd import fused_residual_gate_rms_norm_modulate, fused_rms_norm_modulate, quant
 
     cols = HIDDEN
     gen = torch.Generator(device=dev).manual_seed(10)
@@ -392,7 +393,17 @@ def bench_adaln(torch, dev, steps, warmup):
     _, pre_ms = time_steps(torch, lambda: fused_rms_norm_modulate(x, w, t[1], t[0], idx, 1e-6), steps, warmup)
     _, post_ms = time_steps(
         torch, lambda: fused_residual_gate_rms_norm_modulate(x, branch, t[2], w, t[4], t[3], idx, 1e-6), steps, warmup)
-    return {"rms_norm_modulate": (pre_ms, 2 * row_bytes), "residual_gate_rms_norm_modulate": (post_ms, 4 * row_bytes)}
+    # as in the DiT block: the modulated rows go straight into the next projection's token quant
+    q8 = torch.empty((LQ, cols), dtype=torch.int8, device=dev)
+    s8 = torch.empty((LQ, 1), dtype=torch.float32, device=dev)
+
+    def gate_then_quant():
+        _, out = fused_residual_gate_rms_norm_modulate(x, branch, t[2], w, t[4], t[3], idx, 1e-6)
+        quant.dynamic_scaled_int8_quant(q8, out, s8)
+
+    _, pair_ms = time_steps(torch, gate_then_quant, steps, warmup)
+    return {"rms_norm_modulate": (pre_ms, 2 * row_bytes), "residual_gate_rms_norm_modulate": (post_ms, 4 * row_bytes),
+            "residual_gate_then_token_quant": (pair_ms, 4 * row_bytes + 3 * LQ * cols)}
 
 
 def _cpu_threads(torch) -> dict:

@@ -121,8 +121,9 @@ __global__ void __launch_bounds__(256) row_kernel(const RowArgs a) {
         v[i] = h;
         if constexpr (OP == kGate)
           *(i32x4 *)(a.out + row * a.out_stride + 8 * c) = h;
-        else
-          *(i32x4 *)(a.hidden + row * a.hidden_stride + 8 * c) = h;
+        else  // the new residual stream, read again only after the attention and the MLP: a
+              // non-temporal store keeps it from evicting `out`, which the next kernel reads at once
+          __builtin_nontemporal_store(h, (i32x4 *)(a.hidden + row * a.hidden_stride + 8 * c));
       }
     }
     if constexpr (OP == kGate) return;
