@@ -456,45 +456,99 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
   for (int r = 0; r < 8; ++r) cur[r] = read_op(0, 0, r);
 
-  // k block d at ring position dm: k-steps 0..3.  Unit 2 d + 4 is loaded under
-  // k-step 0 and unit 2 d + 5 under k-step 3, one load per two MFMAs.  One
-  // barrier, in front of k-step 3: behind it, units 2 d + 2 and 2 d + 3 (block
-  // d + 1) have landed for k-step 3 to read ahead from, and nobody reads
-  // block d's units any more (k-step 3's operands are already in registers),
-  // so their slots take units 2 d + 5 and 2 d + 6.
-  auto block = [&](auto dm_c, int d) {
-    constexpr int dm = decltype(dm_c)::value, dn = (dm + 1) % HRING;
+  // Epilogue operands: the column scales and bias of n-block i (the lane's
+  // columns n = n0 + wn 128 + 32 i + 8 u + 4 g + (0..3), u = 0..3) and the
+  // row scales of the lane's 4 m-blocks.  The staged epilogue loads n-block
+  // i + 1's while it converts n-block i; a tile that lies inside the matrix in
+  // n loads n-block 0's and the row scales during its last k block, so that
+  // their latency hides under its MFMAs.
+  const bool early = !RAW && !SPLIT && ga.vec_ok && n0 + HBN <= ga.n;
+  float asv[4];
+  f32x4 bsc[4], bsn[4];
+  i32x2 bic[4], bin[4];
+  auto load_row_scales = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) asv[j] = ga.as[min(m0 + wm * 128 + j * 32 + lr, ga.m - 1)];
+  };
+  // VEC: the whole tile lies inside the matrix in n and the scales and bias
+  // are aligned for vector loads (`early`)
+  auto load_cols = [&](auto vec_c, int i, f32x4 *bs, i32x2 *bi) {
+    constexpr bool VEC = decltype(vec_c)::value;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
+      if (VEC || (ga.vec_ok && n + 3 < ga.n)) {
+        bs[u] = *(const f32x4 *)(ga.bs + n);
+        bi[u] = ga.bias ? *(const i32x2 *)(ga.bias + n) : i32x2{0, 0};
+      } else {
+        uint16_t bb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int nn = min(n + e, ga.n - 1);
+          bs[u][e] = ga.bs[nn];
+          bb[e] = ga.bias ? ga.bias[nn] : 0;
+        }
+        bi[u] = i32x2{(int)((uint32_t)bb[0] | ((uint32_t)bb[1] << 16)), (int)((uint32_t)bb[2] | ((uint32_t)bb[3] << 16))};
+      }
+    }
+  };
+
+  // k block d at ring position dm: k-steps 0..3.  MODE 0: unit 2 d + 4 is
+  // loaded under k-step 0 and unit 2 d + 5 under k-step 3, one load per two
+  // MFMAs; one barrier, in front of k-step 3: behind it, units 2 d + 2 and
+  // 2 d + 3 (block d + 1) have landed for k-step 3 to read ahead from, and
+  // nobody reads block d's units any more (k-step 3's operands are already in
+  // registers), so their slots take units 2 d + 5 and 2 d + 6.  The last two
+  // blocks load no units (none are left): MODE 1 (next to last) waits for all
+  // of its loads before the barrier; MODE 2 (last) reads nothing ahead, needs
+  // no barrier, and loads the first epilogue operands.
+  auto block = [&](auto dm_v, auto mode_c, int d) {
+    constexpr int MODE = decltype(mode_c)::value;
+    const int dm = dm_v, dn = (dm + 1) % HRING;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      if (q == 3) {
-        __builtin_amdgcn_s_waitcnt(0x0f70 | 8);  // vmcnt(8): unit 2 d + 4 may stay in flight
+      if (q == 3 && MODE != 2) {
+        if (MODE == 0)
+          __builtin_amdgcn_s_waitcnt(0x0f70 | 8);  // vmcnt(8): unit 2 d + 4 may stay in flight
+        else
+          __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): block d + 1 has landed
         __syncthreads();
       }
+      if constexpr (MODE == 2 && !RAW && !SPLIT)
+        if (q == 0 && early) {
+          load_row_scales();
+          load_cols(std::true_type{}, 0, bsc, bic);
+        }
 #pragma unroll
       for (int idx = 0; idx < 16; ++idx) {
-        if (idx < 8) nxt[idx] = q < 3 ? read_op(dm, q + 1, idx) : read_op(dn, 0, idx);
-        if (q == 0 && idx % 2 == 0) load_one(2 * d + 4, idx / 2);
-        if (q == 3 && idx % 2 == 0) load_one(2 * d + 5, idx / 2);
+        if (idx < 8 && !(MODE == 2 && q == 3)) nxt[idx] = q < 3 ? read_op(dm, q + 1, idx) : read_op(dn, 0, idx);
+        if (MODE == 0 && q == 0 && idx % 2 == 0) load_one(2 * d + 4, idx / 2);
+        if (MODE == 0 && q == 3 && idx % 2 == 0) load_one(2 * d + 5, idx / 2);
         const int nb = idx >> 2, mb = idx & 3;
         acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[4 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
+      if (!(MODE == 2 && q == 3))
 #pragma unroll
-      for (int r = 0; r < 8; ++r) cur[r] = nxt[r];
+        for (int r = 0; r < 8; ++r) cur[r] = nxt[r];
     }
   };
+  using M0 = std::integral_constant<int, 0>;
   int d = 0;
-  for (; d + HRING <= nd; d += HRING) {
-    block(std::integral_constant<int, 0>{}, d);
-    block(std::integral_constant<int, 1>{}, d + 1);
-    block(std::integral_constant<int, 2>{}, d + 2);
-    block(std::integral_constant<int, 3>{}, d + 3);
-    block(std::integral_constant<int, 4>{}, d + 4);
+  for (; d + HRING <= nd - 2; d += HRING) {
+    block(std::integral_constant<int, 0>{}, M0{}, d);
+    block(std::integral_constant<int, 1>{}, M0{}, d + 1);
+    block(std::integral_constant<int, 2>{}, M0{}, d + 2);
+    block(std::integral_constant<int, 3>{}, M0{}, d + 3);
+    block(std::integral_constant<int, 4>{}, M0{}, d + 4);
   }
-  if (d < nd) block(std::integral_constant<int, 0>{}, d);
-  if (d + 1 < nd) block(std::integral_constant<int, 1>{}, d + 1);
-  if (d + 2 < nd) block(std::integral_constant<int, 2>{}, d + 2);
-  if (d + 3 < nd) block(std::integral_constant<int, 3>{}, d + 3);
+  if (d < nd - 2) block(std::integral_constant<int, 0>{}, M0{}, d);
+  if (d + 1 < nd - 2) block(std::integral_constant<int, 1>{}, M0{}, d + 1);
+  if (d + 2 < nd - 2) block(std::integral_constant<int, 2>{}, M0{}, d + 2);
+  if (d + 3 < nd - 2) block(std::integral_constant<int, 3>{}, M0{}, d + 3);
+  // the last two blocks, at ring positions known at run time only
+  if (nd >= 2) block((nd - 2) % HRING, std::integral_constant<int, 1>{}, nd - 2);
+  block((nd - 1) % HRING, std::integral_constant<int, 2>{}, nd - 1);
   // every wave drains its loads before the workgroup ends
   __builtin_amdgcn_s_waitcnt(0x0f70);
 
@@ -516,31 +570,6 @@ gemm_i8_wave128_kernel(const GArgs ga) {
     return;
   }
 
-  // epilogue: lane holds m = m-block base + lr; n = n-block base + 8u + 4g + (0..3).
-  // The column scales and bias of the lane's 16 n-groups are loaded once.
-  f32x4 bsv[4][4];
-  i32x2 biv[4][4];
-  if constexpr (!RAW) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
-        if (ga.vec_ok && n + 3 < ga.n) {
-          bsv[i][u] = *(const f32x4 *)(ga.bs + n);
-          biv[i][u] = ga.bias ? *(const i32x2 *)(ga.bias + n) : i32x2{0, 0};
-        } else {
-          uint16_t bb[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int nn = min(n + e, ga.n - 1);
-            bsv[i][u][e] = ga.bs[nn];
-            bb[e] = ga.bias ? ga.bias[nn] : 0;
-          }
-          biv[i][u] = i32x2{(int)((uint32_t)bb[0] | ((uint32_t)bb[1] << 16)), (int)((uint32_t)bb[2] | ((uint32_t)bb[3] << 16))};
-        }
-      }
-  }
   if constexpr (!RAW) {
     if (ga.st_ok) {
       // bf16 tile through LDS: each wave stages its 128 x 128 outputs in rows
@@ -549,22 +578,25 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       static_assert(HWAVES * 128 * ROWB <= HRING * HUNIT, "staging fits the ring");
       __syncthreads();  // every wave is done with the ring
       const uint32_t wt = (uint32_t)(w * 128 * ROWB);
-      float asv[4];  // row scales of the lane's 4 m-blocks
-#pragma unroll
-      for (int j = 0; j < 4; ++j) asv[j] = ga.as[min(m0 + wm * 128 + j * 32 + lr, ga.m - 1)];
+      if (!early) {
+        load_row_scales();
+        load_cols(std::false_type{}, 0, bsc, bic);
+      }
       // n-blocks outermost, so that one block's column scales and converted
-      // bias are live at a time, and the bias test outside the element loops
-      // (per element: convert, two multiplies, the bias add, half a pack)
-      auto stage_tile = [&](auto has_bias) {
+      // bias are live at a time (the next block's are in flight), and the
+      // bias test outside the element loops (per element: convert, two
+      // multiplies, the bias add, half a pack)
+      auto stage_tile = [&](auto has_bias, auto vec_c) {
         constexpr bool HB = decltype(has_bias)::value;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          if (i < 3) load_cols(vec_c, i + 1, bsn, bin);
           float bf[4][4];
 #pragma unroll
           for (int u = 0; u < 4; ++u)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
+              const uint32_t bw = (uint32_t)bic[u][e >> 1];
               bf[u][e] = HB ? bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu)) : 0.0f;
             }
 #pragma unroll
@@ -576,7 +608,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
               for (int e = 0; e < 4; ++e) {
                 float t = (float)acc[i][j][4 * u + e];
-                t = t * bsv[i][u][e];
+                t = t * bsc[u][e];
                 t = t * asv[j];
                 if constexpr (HB) t = t + bf[u][e];
                 tv[e] = t;
@@ -586,12 +618,24 @@ gemm_i8_wave128_kernel(const GArgs ga) {
                   i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
                         (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
             }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            bsc[u] = bsn[u];
+            bic[u] = bin[u];
+          }
         }
       };
-      if (ga.bias)
-        stage_tile(std::true_type{});
-      else
-        stage_tile(std::false_type{});
+      if (early) {
+        if (ga.bias)
+          stage_tile(std::true_type{}, std::true_type{});
+        else
+          stage_tile(std::false_type{}, std::true_type{});
+      } else {
+        if (ga.bias)
+          stage_tile(std::true_type{}, std::false_type{});
+        else
+          stage_tile(std::false_type{}, std::false_type{});
+      }
       if constexpr (GLU) {
         // gate halves sit in the staging rows of waves (wm, 0), up halves in
         // (wm, 1); each wave writes 64 of the tile's 256 output rows
@@ -628,13 +672,15 @@ gemm_i8_wave128_kernel(const GArgs ga) {
     }
   }
   if constexpr (GLU) return;  // the GLU launcher always takes the staged path above
+  // unstaged epilogue (bf16 rows not 16-byte aligned) and the raw int32 output
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int m = m0 + wm * 128 + j * 32 + lr;
-    if (m >= ga.m) continue;
-    const float asm_ = RAW ? 0.0f : ga.as[m];
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (!RAW) load_cols(std::false_type{}, i, bsc, bic);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int j = 0; j < 4; ++j) {
+      const int m = m0 + wm * 128 + j * 32 + lr;
+      if (m >= ga.m) continue;
+      const float asm_ = RAW ? 0.0f : ga.as[m];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
@@ -653,10 +699,10 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float t = (float)acc[i][j][4 * u + e];
-            t = t * bsv[i][u][e];
+            t = t * bsc[u][e];
             t = t * asm_;
             if (ga.bias) {
-              const uint32_t bw = (uint32_t)biv[i][u][e >> 1];
+              const uint32_t bw = (uint32_t)bic[u][e >> 1];
               t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
             }
             tv[e] = t;
