@@ -443,7 +443,7 @@ def _cpu_attention_heads(torch, fn, lq, segs, gen, heads_list=(1, 4)):
 
 
 def cpu_baseline(torch):
-    """The reference's CPU path on the host cores, BASELINE's protocol: 1
+    """The reference's CPU path on the host cores: 1
     warm-up, median of 3 runs, 1 and 4 heads timed, the 40-head call
     extrapolated linearly (marked as such).
 

@@ -3,7 +3,7 @@
 TEST INFRASTRUCTURE ONLY.  This package restates, on the CPU, the arithmetic
 of the reference path so the HIP implementation can be checked against it.
 Only tests/, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-bench.py may import it, and only as the checker or the timed CPU baseline;
+bench.py may import it, and only to check results or as the timed CPU baseline;
 the product package (``taomate_hd_amd``) never imports it and has no CPU
 fallback.
 

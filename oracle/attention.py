@@ -73,7 +73,7 @@ def i8qk_attention(q: np.ndarray, k_segments: list[np.ndarray], v_segments: list
     """INT8-QK attention of ``q [Lq, H, D]`` over the given key/value segments.
 
     Restates the accelerated backend (attention_hook.py:335-371,
-    sage_value_padding.py:79-97) with the BASELINE quantization: smooth-K mean
+    sage_value_padding.py:79-97) with the INT8-QK workload's quantization: smooth-K mean
     over all keys of the call, per-128-block INT8 Q and K (K blocks restart at
     each segment), logits = (q_i8 . k_i8) * s_q * s_k * scale exactly, then a
     float64 softmax and P.V.  Returns (out [Lq, H, D] float64, operands dict).

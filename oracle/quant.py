@@ -23,7 +23,7 @@ def token_quant(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     src/taomate_hd/inference/w8a8.py:71 (and ``scaled_int8_quant`` at :141):
       scale[m] = amax_m / 127 (fp32),  q = sat_int8(rint(x * (127 / amax_m)))
     The vLLM source is not in the container; the formula is the one recalled
-    from its public kernel, stated in include/tmhd.h and owned by this build.
+    from its public kernel and stated in include/tmhd.h.
     amax = 0 gives scale 0 and q 0.
     Pinned by tests/test_oracle.py (closed forms: max element -> +-127, error
     bound <= scale/2, ties to even, zero rows).
@@ -114,8 +114,8 @@ def block_quant(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
     """Per-(128-row block, head) symmetric INT8 quantization of ``x [N, H, D]``.
 
     SageAttention's per-block INT8 Q/K quantization
-    (sage_value_padding.py:90-92 calls its per-thread variant; BASELINE's
-    config 4 fixes 128-token blocks).  Formula stated in include/tmhd.h:
+    (sage_value_padding.py:90-92 calls its per-thread variant; the INT8-QK
+    workload fixes 128-token blocks).  Formula stated in include/tmhd.h:
       scale = amax / 127,  q = sat_int8(rint(x * (127 / amax))),  amax = 0 -> 0.
     Returns q [N, H, D] int8 and scale [H, ceil(N / 128)] float32.
     Pinned by tests/test_oracle.py (as token_quant, per block).

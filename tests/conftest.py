@@ -44,7 +44,7 @@ def torch_mod():
 def dev(torch_mod):
     from taomate_hd_amd import _native
 
-    _native.load()  # fail loudly if the HIP library is missing on a GPU box
+    _native.load()  # fail loudly if the HIP library is missing where a GPU is present
     return torch_mod.device("cuda:0")
 
 

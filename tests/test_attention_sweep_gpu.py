@@ -80,7 +80,7 @@ def test_random_attention_case_matches_oracle(torch_mod, dev, case):
         want, _ = oatt.i8qk_attention(q, ksegs, vsegs, dim ** -0.5)
         if not case["peaky"]:  # Q x 4 also scales the quantisation error of the logits
             assert oatt.cosine(got, exact) >= 0.999
-    # BASELINE gate: 2e-2 max, 1e-3 mean abs; with a few keys the output is O(1) and
+    # BF16 gate: 2e-2 max, 1e-3 mean abs; with a few keys the output is O(1) and
     # its own bf16 rounding alone can average 1e-3, so the mean gate is at least 1.5 x that
     mean_round = float(np.abs(bf16.round_f32(want.astype(np.float32)) - want).mean())
     mx, mean = err_stats(got, want)

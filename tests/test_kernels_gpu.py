@@ -12,7 +12,7 @@ from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
 
 pytestmark = pytest.mark.gpu
 
-# BF16 attention gate (BASELINE): max abs <= 2e-2 and mean abs <= 1e-3 vs fp32/fp64 SDPA
+# BF16 attention gate: max abs <= 2e-2 and mean abs <= 1e-3 vs fp32/fp64 SDPA
 BF16_MAX_ABS = 2e-2
 BF16_MEAN_ABS = 1e-3
 # INT8-QK gate: cosine >= 0.999 vs fp32 SDPA on the unquantized inputs

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle before it is trusted as the checker.
+"""Pins the CPU oracle before the kernels are compared against it.
 
 The reference ships no tests, fixtures or golden vectors for this path, so
 each oracle function is pinned by closed forms, invariants, brute force on
