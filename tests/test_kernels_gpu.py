@@ -330,20 +330,23 @@ def test_gemm_split_round_equals_unsplit(torch_mod, dev):
 
 @pytest.mark.parametrize("backend", ["bf16", "i8qk"])
 @pytest.mark.parametrize(
-    "lq,splits",
+    "H,lq,splits",
     [
-        (4836, [1560, 4836, 4836, 4836]),  # 480p stage: Lkv 16,068 (anchor + two history chunks + self)
-        (12252, [4032, 12252, 12252, 12252]),  # 768p stage: Lkv 40,788
+        (40, 4836, [1560, 4836, 4836, 4836]),  # 480p stage: Lkv 16,068 (anchor + two history chunks + self)
+        (40, 12252, [4032, 12252, 12252, 12252]),  # 768p stage: Lkv 40,788
+        # the model's own 768p call on one GPU's 14 heads: 10 x 1,032 video + 2 x 57 audio queries over a
+        # 12-latent video sink, two history chunks and the chunk itself (Lkv 43,686; 574 items, split last round)
+        (14, 10434, [12384, 10434, 10434, 10434]),
     ],
 )
-def test_full_size_stage_shapes_on_sampled_rows(torch_mod, dev, backend, lq, splits):
-    """The stage shapes at full size (40 heads, head_dim 128): the whole
-    attention runs; 64 query rows of 3 heads are checked against the fp64
-    oracle over every key (BF16 gate, or the INT8-QK cosine gate)."""
+def test_full_size_stage_shapes_on_sampled_rows(torch_mod, dev, backend, H, lq, splits):
+    """The stage shapes at full size (head_dim 128): the whole attention
+    runs; 64 query rows of 3 heads are checked against the fp64 oracle over
+    every key (BF16 gate, or the INT8-QK cosine gate)."""
     torch = torch_mod
     from taomate_hd_amd import KVSlot, segment_attention
 
-    H, D = 40, 128
+    D = 128
     n = sum(splits)
     gen = torch.Generator(device=dev).manual_seed(lq)
     q = torch.randn(lq, H, D, generator=gen, device=dev).to(torch.bfloat16)
@@ -360,7 +363,7 @@ def test_full_size_stage_shapes_on_sampled_rows(torch_mod, dev, backend, lq, spl
     torch.cuda.synchronize()
     rng = np.random.default_rng(lq)
     rows = np.unique(np.concatenate([[0, lq - 1], rng.integers(0, lq, 62)]))
-    heads = [0, 17, 39]
+    heads = [0, H // 2 - 3, H - 1]
     qs = bf16.from_torch(q[torch.tensor(rows, device=dev)][:, heads].contiguous())
     ks = bf16.from_torch(k[:, heads].contiguous())
     vs = bf16.from_torch(v[:, heads].contiguous())
