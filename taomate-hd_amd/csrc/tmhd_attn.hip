@@ -391,12 +391,18 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 //         the next sub-tile's scores, after the score-read guard (costed 4
 //         for BF16, 8 for INT8: below its 12 issue cycles, which spreads the
 //         INT8 units more evenly and measured 1.5-2% faster than 12);
-//   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions.
+//   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions;
+//   X(u): the two exp2 of pair u of the NEXT sub-tile, for its first `nx` / 2
+//         pairs of each half (16, after the score-read guard and the pair's M
+//         unit).  The regions of the last P.V MFMAs hold little else, while the
+//         first regions of every sub-tile are over budget; those pairs then
+//         have no E unit in their own sub-tile (1% faster at nx = 2 on both
+//         backends in a same-box A/B; 4 and 6 gained less).
 // Every region starts with its share of the fixed work (the operand read of
 // odd regions, the wait in front of each slot's first MFMA); each unit goes
 // to the cheapest region of its window (the earliest on ties).
 struct SlotPlan {
-  int e[16], c[16], m[16], l[16];
+  int e[16], c[16], m[16], l[16], x[16];
 };
 constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   int best = lo;
@@ -406,10 +412,12 @@ constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   return best;
 }
 constexpr int kGuardRegionOffset = 1;  // score-read guard in region 2 * nqk + 1
-constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i8) {
+constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i8, int nx) {
   SlotPlan s{};
   int cost[64] = {};
   const int ns = nqk + npv, nr = 2 * ns;
+  auto early = [&](int u) { return (u & 7) < nx / 2; };  // exponentials computed by the previous sub-tile
+  for (int u = 0; u < 16; ++u) s.x[u] = -1;
   for (int i = 0; i < ns; ++i) {
     cost[2 * i] += 4;
     cost[2 * i + 1] += 4;
@@ -418,11 +426,13 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
   for (int q = 0; q < 4; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * nqk + hf - 1;
-      s.e[u] = plan_put(cost, 0, dl, 16);
-      s.c[u] = plan_put(cost, s.e[u], dl, 12);
+      s.e[u] = early(u) ? -1 : plan_put(cost, 0, dl, 16);
+      s.c[u] = plan_put(cost, early(u) ? 0 : s.e[u], dl, 12);
     }
   for (int q = 0; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
+  for (int u = 0; u < 16; ++u)
+    if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
   for (int q = 4; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
@@ -550,8 +560,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   static_assert(NLD <= 16, "slot plan bounds");
   // tile loads spread over the first 1.5 NS regions (BF16) or all of them (INT8: 1.3% faster in a
   // same-box A/B, BF16 unchanged)
-  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : 3 * NS / 2, I8);  // sub-tiles with tile loads
-  constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8);               // sub-tiles without
+  constexpr int NX = 2;  // early exponentials: pair 0 of each query half
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : 3 * NS / 2, I8, NX);  // sub-tiles with tile loads
+  constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8, NX);               // sub-tiles without
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
   auto set_voff = [&](uint32_t vrs2) {
@@ -689,6 +700,19 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   for (int i = 0; i < LA; ++i) pre[i] = lds_read(kro + 32 * KRS + i * 32);
 
   int j = 0, b0 = 0, b1 = 1, b2 = 2;  // LDS buffers of tiles j, j+1, j+2
+  // exp2 of the first NX / 2 pairs of each query half of the next sub-tile's
+  // scores (the X units of the slot plan; for sub-tile 0, here)
+  float pe_early[16][2];
+  auto early_exp = [&](f32x16 (&s)[2], int hf) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if ((u & 7) < NX / 2 && (u >> 3) == hf) {
+        pe_early[u][0] = __builtin_amdgcn_exp2f(s[hf][2 * (u & 7)]);
+        pe_early[u][1] = __builtin_amdgcn_exp2f(s[hf][2 * (u & 7) + 1]);
+      }
+  };
+  early_exp(sA, 0);
+  early_exp(sA, 1);
 
   // One 32-key sub-tile, software-pipelined by hand in NS slots of two MFMAs
   // (one per query half), each MFMA fenced with the units the plan puts in
@@ -719,6 +743,12 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int i = 0; i < LA; ++i) ops[i] = pre[i];
     float pe[2][8][2];  // exponentials of the current sub-tile, between their E and C units
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if ((u & 7) < NX / 2) {  // computed by the previous sub-tile (or the prologue)
+        pe[u >> 3][u & 7][0] = pe_early[u][0];
+        pe[u >> 3][u & 7][1] = pe_early[u][1];
+      }
 #pragma clang loop unroll(full)
     for (int r = 0; r < 2 * NS; ++r) {
       const int i = r >> 1, hr = r & 1;  // slot, query half of MFMA r
@@ -772,6 +802,14 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
           lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][rr], sn[hf][rr + 1]));
           asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this region
         }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.x[u] == r) {
+          const int hf = u >> 3, q = u & 7;
+          pe_early[u][0] = __builtin_amdgcn_exp2f(sn[hf][2 * q]);
+          pe_early[u][1] = __builtin_amdgcn_exp2f(sn[hf][2 * q + 1]);
+          asm volatile("" : "+v"(pe_early[u][0]), "+v"(pe_early[u][1]));  // keeps them in this region
+        }
       __builtin_amdgcn_sched_barrier(0);
       if (i < NQK) {
         if constexpr (I8)
@@ -797,6 +835,8 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       mask_sub(sn, nvo);
       lm[0] = sub_max(sn[0]);
       lm[1] = sub_max(sn[1]);
+      early_exp(sn, 0);  // of the masked scores
+      early_exp(sn, 1);
     }
     if (__any(fmaxf(lm[0], lm[1]) > kLazyRescale)) {
       mfma_drain();
@@ -810,6 +850,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         for (int db = 0; db < DB; ++db) orescale(hf * DB + db, o[hf][db], alpha);
         sn[hf] -= delta;
         mref[hf] += delta;
+        early_exp(sn, hf);  // against the new reference
         negm[hf] = -mref[hf];
         if constexpr (!I8) npin(hf, negm[hf]);
       }
