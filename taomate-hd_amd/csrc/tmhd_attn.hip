@@ -394,10 +394,10 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 //   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions;
 //   X(u): the two exp2 of pair u of the NEXT sub-tile, for its first `nx` / 2
 //         pairs of each half (16, after the score-read guard and the pair's M
-//         unit).  The regions of the last P.V MFMAs hold little else, while the
-//         first regions of every sub-tile are over budget; those pairs then
-//         have no E unit in their own sub-tile (1% faster at nx = 2 on both
-//         backends in a same-box A/B; 4 and 6 gained less).
+//         unit), placed after every other unit: the regions of the last P.V
+//         MFMAs hold little else, while the first regions of every sub-tile
+//         are over budget; those pairs then have no E unit in their own
+//         sub-tile.
 // Every region starts with its share of the fixed work (the operand read of
 // odd regions, the wait in front of each slot's first MFMA); each unit goes
 // to the cheapest region of its window (the earliest on ties).
@@ -431,8 +431,7 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
     }
   for (int q = 0; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
-  for (int u = 0; u < 16; ++u)
-    if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
+
   for (int q = 4; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
@@ -440,6 +439,8 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
       s.c[u] = plan_put(cost, s.e[u], dl, 12);
     }
   for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 8) : -1;
+  for (int u = 0; u < 16; ++u)
+    if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
   return s;
 }
 
@@ -560,7 +561,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   static_assert(NLD <= 16, "slot plan bounds");
   // tile loads spread over the first 1.5 NS regions (BF16) or all of them (INT8: 1.3% faster in a
   // same-box A/B, BF16 unchanged)
-  constexpr int NX = 2;  // early exponentials: pair 0 of each query half
+  // early exponentials: pairs 0..3 of each query half (same-box A/B at 768p, 6 runs each, against
+  // pair 0 placed before the second E / C units: BF16 8.098 -> 7.995 ms, INT8-QK 7.314 -> 7.279 ms;
+  // pair 0 alone, placed last: 8.036 / 7.294 ms; against no early units, pair 0 gave about 1%)
+  constexpr int NX = 8;
   constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : 3 * NS / 2, I8, NX);  // sub-tiles with tile loads
   constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8, NX);               // sub-tiles without
   // value source offsets for the V^T row stride of the current load segment
