@@ -387,6 +387,10 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 //         the current sub-tile (8 each);
 //   C(u): their bf16 pack and row-sum adds (4 each), at or after E(u) and at
 //         least one MFMA before the P.V MFMA that reads the pack;
+//   A(u): INT8 only, the row-sum adds of pair u, split from its pack: placed
+//         after the tile loads, anywhere after C(u) (for the early pairs
+//         below, in front of the score guard, so before any X unit):
+//         1-1.6% faster in a same-box A/B;
 //   M(u): INT8 dequantisation and row maximum of pair u % 8, half u / 8 of
 //         the next sub-tile's scores, after the score-read guard (costed 4
 //         for BF16, 8 for INT8: below its 12 issue cycles, which spreads the
@@ -402,7 +406,7 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 // odd regions, the wait in front of each slot's first MFMA); each unit goes
 // to the cheapest region of its window (the earliest on ties).
 struct SlotPlan {
-  int e[16], c[16], m[16], l[16], x[16];
+  int e[16], c[16], m[16], l[16], x[16], a[16];
 };
 constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   int best = lo;
@@ -427,7 +431,7 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * nqk + hf - 1;
       s.e[u] = early(u) ? -1 : plan_put(cost, 0, dl, 16);
-      s.c[u] = plan_put(cost, early(u) ? 0 : s.e[u], dl, 12);
+      s.c[u] = plan_put(cost, early(u) ? 0 : s.e[u], dl, i8 ? 4 : 12);
     }
   for (int q = 0; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
@@ -436,9 +440,10 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
       s.e[u] = plan_put(cost, 0, dl, 16);
-      s.c[u] = plan_put(cost, s.e[u], dl, 12);
+      s.c[u] = plan_put(cost, s.e[u], dl, i8 ? 4 : 12);
     }
   for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 8) : -1;
+  for (int u = 0; u < 16; ++u) s.a[u] = i8 ? plan_put(cost, s.c[u], early(u) ? 2 * nqk + 1 : nr - 1, 8) : -1;
   for (int u = 0; u < 16; ++u)
     if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
   return s;
@@ -781,11 +786,22 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         if (pl.c[u] == r) {
           const int hf = u >> 3, q = u & 7;
           int pr = (int)pack_bf16x2(pe[hf][q][0], pe[hf][q][1]);
-          ts[hf] += pe[hf][q][0];
-          ts[hf] += pe[hf][q][1];
+          if constexpr (!I8) {
+            ts[hf] += pe[hf][q][0];
+            ts[hf] += pe[hf][q][1];
+          }
           asm volatile("" : "+v"(pr), "+v"(ts[hf]));  // keeps the pack and the row sum in this region
           pk[hf][q >> 2][q & 3] = pr;
         }
+      if constexpr (I8)
+#pragma unroll
+        for (int u = 0; u < 16; ++u)
+          if (pl.a[u] == r) {
+            const int hf = u >> 3, q = u & 7;
+            ts[hf] += pe[hf][q][0];
+            ts[hf] += pe[hf][q][1];
+            asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this region
+          }
       if (r == 2 * NQK + kGuardRegionOffset) {
         // first reads of the next sub-tile's scores: at least 12 wait states
         // after the last score MFMA (the MFMA in front of this region and
