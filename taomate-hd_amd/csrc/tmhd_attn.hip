@@ -564,13 +564,14 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // load n of a tile: K blocks first (n < KWL), then V blocks
   constexpr int NLD = KWL + VWL;
   static_assert(NLD <= 16, "slot plan bounds");
-  // tile loads spread over the first 1.5 NS regions (BF16) or all of them (INT8: 1.3% faster in a
-  // same-box A/B, BF16 unchanged)
+  // tile loads spread over the first NS regions (BF16: with the early exponentials in the last
+  // regions, 0.7% faster than 1.5 NS in two same-box A/Bs, 2 NS 1.3% slower) or over all of them
+  // (INT8: 1.3% faster in a same-box A/B)
   // early exponentials: pairs 0..3 of each query half (same-box A/B at 768p, 6 runs each, against
   // pair 0 placed before the second E / C units: BF16 8.098 -> 7.995 ms, INT8-QK 7.314 -> 7.279 ms;
   // pair 0 alone, placed last: 8.036 / 7.294 ms; against no early units, pair 0 gave about 1%)
   constexpr int NX = 8;
-  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : 3 * NS / 2, I8, NX);  // sub-tiles with tile loads
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : NS, I8, NX);  // sub-tiles with tile loads
   constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8, NX);               // sub-tiles without
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
