@@ -435,7 +435,6 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
     }
   for (int q = 0; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
-
   for (int q = 4; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
@@ -447,6 +446,29 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
   for (int u = 0; u < 16; ++u)
     if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
   return s;
+}
+
+// The orderings the sub-tile code relies on, checked at compile time:
+// a pair's pack after its exponentials and by its P.V deadline; maxima and
+// early exponentials after the score guard (the early ones of INT8 after
+// their pair's dequantisation); INT8 adds after the pack and, for early
+// pairs, in front of the guard (so before any X unit rewrites the carried
+// exponentials); loads inside their window.
+constexpr bool plan_valid(const SlotPlan &s, int nqk, int npv, int db, int nld, int lwin, bool i8, int nx) {
+  const int nr = 2 * (nqk + npv), guard = 2 * nqk + kGuardRegionOffset;
+  for (int u = 0; u < 16; ++u) {
+    const int hf = u >> 3, q = u & 7;
+    const bool early = q < nx / 2;
+    const int dl = q < 4 ? 2 * nqk + hf - 1 : 2 * (nqk + db) + hf - 1;
+    if (early != (s.e[u] < 0) || s.c[u] < (early ? 0 : s.e[u]) || s.c[u] > dl) return false;
+    if (s.m[u] <= guard || s.m[u] >= nr) return false;
+    if (early != (s.x[u] >= 0) || (early && (s.x[u] <= guard || s.x[u] < (i8 ? s.m[u] : 0) || s.x[u] >= nr)))
+      return false;
+    if (i8 != (s.a[u] >= 0) || (i8 && (s.a[u] < s.c[u] || s.a[u] >= (early ? guard + 1 : nr)))) return false;
+  }
+  for (int n = 0; n < 16; ++n)
+    if ((n < nld) != (s.l[n] >= 0) || s.l[n] >= lwin) return false;
+  return true;
 }
 
 template <int D, bool I8>
@@ -573,6 +595,8 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   constexpr int NX = 8;
   constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : NS, I8, NX);  // sub-tiles with tile loads
   constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8, NX);               // sub-tiles without
+  static_assert(plan_valid(PL, NQK, NPV, DB, NLD, I8 ? 2 * NS : NS, I8, NX) && plan_valid(PN, NQK, NPV, DB, 0, 1, I8, NX),
+                "slot plan orderings");
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
   auto set_voff = [&](uint32_t vrs2) {
