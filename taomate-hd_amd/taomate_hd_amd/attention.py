@@ -15,7 +15,7 @@ from typing import Any, Sequence
 
 from . import _native
 from .profiling import ComponentTimer, maybe_region
-from .slots import KV_TILE, SlotView, round_up
+from .slots import KV_TILE, KVSlot, SlotView, round_up, vt_columns
 
 BACKENDS = ("bf16", "i8qk")
 
@@ -158,6 +158,27 @@ def _key_sum(torch: Any, lib: Any, view: SlotView, stream: int) -> int:
     return _native.ptr(hit)
 
 
+def _coalesce_segments(torch: Any, segments: list[SlotView], limit: int) -> list[SlotView]:
+    """One launch takes at most ``limit`` segments; the reference has no such
+    bound (it concatenates every part).  With more, the oldest segments are
+    copied, in order, into one temporary slot: their keys stay the same keys,
+    so the result is the attention over the same set (the INT8-QK key blocks
+    then run over the merged rows, as they run over any segment)."""
+    n_merge = len(segments) - limit + 1
+    head, rest = segments[:n_merge], segments[n_merge:]
+    keys, values = [], []
+    for view in head:
+        slot, r0, n = view.slot, int(view.row0), int(view.tokens)
+        keys.append(slot.k[:, r0 : r0 + n, :].permute(1, 0, 2))
+        cols = r0 + vt_columns(torch, n, slot.device)  # r0 is a multiple of 64: whole 16-token groups
+        values.append(slot.vt.index_select(2, cols).permute(2, 0, 1))
+    key, value = torch.cat(keys, 0).contiguous(), torch.cat(values, 0).contiguous()
+    first = head[0].slot
+    merged = KVSlot(torch, heads=first.heads, head_dim=first.head_dim, capacity=int(key.shape[0]), device=first.device)
+    merged.pack(key, value)
+    return [merged.view(), *rest]
+
+
 def segment_attention(
     torch: Any,
     query: Any,
@@ -220,11 +241,11 @@ def segment_attention(
     segments = [s for s in segments if s.tokens > 0]
     if not segments:
         raise ValueError("attention needs at least one key/value token")
-    if len(segments) > _native.MAX_SEGMENTS:
-        raise ValueError(f"at most {_native.MAX_SEGMENTS} key/value segments per call")
     for s in segments:
         if s.slot.heads != heads or s.slot.head_dim != head_dim or s.slot.device != query.device:
             raise ValueError("segment heads/dim/device differ from the query")
+    if len(segments) > _native.MAX_SEGMENTS:
+        segments = _coalesce_segments(torch, segments, _native.MAX_SEGMENTS)
     args = _native.AttnArgs()
     args.q = _native.ptr(query)
     args.q_token_stride = query.stride(0)

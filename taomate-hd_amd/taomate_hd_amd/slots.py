@@ -35,6 +35,14 @@ def vt_position(t: int) -> int:
     return (t & ~15) | (perm << 2) | (t & 3)
 
 
+def vt_columns(torch: Any, count: int, device: Any) -> Any:
+    """``vt_position`` of tokens ``0 .. count - 1`` as a long tensor on ``device``."""
+    t = torch.arange(int(count), device=device)
+    chunk = (t >> 2) & 3
+    perm = torch.where(chunk == 1, 2, torch.where(chunk == 2, 1, chunk))
+    return (t & ~15) | (perm << 2) | (t & 3)
+
+
 @dataclass
 class SlotView:
     """Rows ``row0 .. row0 + tokens`` of a slot, as one attention segment.
@@ -137,7 +145,7 @@ class KVSlot:
         torch = self._torch
         n = self.tokens if tokens is None else int(tokens)
         key = self.k[:, :n, :].permute(1, 0, 2).contiguous()
-        cols = torch.tensor([vt_position(t) for t in range(n)], dtype=torch.long, device=self.device)
+        cols = vt_columns(torch, n, self.device)
         value = self.vt.index_select(2, cols).permute(2, 0, 1).contiguous()
         if order is not None:
             key = key.index_select(0, order)

@@ -402,3 +402,50 @@ def test_condition_cache_cached_rows_and_compact_output(torch_mod, dev, backend)
         wk, wv = ocache.history(layer)
         assert np.array_equal(bf16.from_torch(pair.key), wk)
         assert np.array_equal(bf16.from_torch(pair.value), wv)
+
+
+@pytest.mark.parametrize("backend", ["sdpa", "sage_attn"])
+def test_stream_without_retention_beyond_one_launch(torch_mod, dev, backend, monkeypatch):
+    """Every committed block kept (the reference's cache has no bound on the
+    history it concatenates): after 15 blocks the media queries see more
+    segments than one launch takes and the oldest are merged into one
+    temporary slot; the outputs still follow the oracle hook call for call."""
+    torch = torch_mod
+    from taomate_hd_amd import HeadMajorRingKVCache, KVContract, StreamingAttentionHook
+    from taomate_hd_amd.hook import HookMode
+
+    from taomate_hd_amd import attention as attn_mod
+
+    merges = []
+    coalesce = attn_mod._coalesce_segments
+    monkeypatch.setattr(attn_mod, "_coalesce_segments", lambda *a: merges.append(len(a[1])) or coalesce(*a))
+    layer = LAYERS[0]
+    cache = HeadMajorRingKVCache(KVContract(layer_names=(layer,), local_heads=H, head_dim=D))
+    hook = StreamingAttentionHook(cache, attention_backend=backend)
+    ocache, exact_cache = ost.CacheOracle((layer,)), ost.CacheOracle((layer,))
+    ohook = ost.HookOracle(ocache, backend=backend)
+    exact_hook = ost.HookOracle(exact_cache, backend="sdpa")
+    tags, mask, bounds = ost.packed_layout(5, 4, 3, 21)
+    T = len(tags)
+    seed = 4000
+    for block in range(20):
+        for mode in ("noisy", "clean_commit"):
+            if mode == "clean_commit":
+                for c in (cache, ocache, exact_cache):
+                    c.begin_clean_commit(block)
+            hook.activate(mode=HookMode(mode), block_index=block)
+            ohook.activate(mode, block)
+            exact_hook.activate(mode, block)
+            q, k, v = _qkv(T, seed)
+            seed += 10
+            got, want = _call(torch, dev, hook, ohook, layer, q, k, v, tags, mask, bounds)
+            exact = exact_hook(layer, q, k, v, tags, mask, bounds, D ** -0.5)
+            _check(backend, got, want if backend == "sdpa" else None, exact)
+            hook.deactivate()
+            ohook.deactivate()
+            exact_hook.deactivate()
+            if mode == "clean_commit":
+                for c in (cache, ocache, exact_cache):
+                    c.commit()
+    assert cache.retained_blocks == 20
+    assert merges and max(merges) > 20  # the last calls merged segments

@@ -406,3 +406,12 @@ def test_row_lists_are_range_checked_before_the_int32_cast_without_gpu():
         _row_list(torch, torch.tensor([0.0, 1.0]), "cpu", 10, "rows", False)
     rows = _row_list(torch, torch.tensor([3, 9], dtype=torch.int64), "cpu", 10, "rows", False)
     assert rows.dtype == torch.int32 and rows.tolist() == [3, 9]
+
+
+def test_vt_columns_match_vt_position():
+    import torch
+
+    from taomate_hd_amd.slots import vt_columns, vt_position
+
+    for n in (0, 1, 15, 16, 17, 63, 64, 65, 1000):
+        assert vt_columns(torch, n, "cpu").tolist() == [vt_position(t) for t in range(n)], n

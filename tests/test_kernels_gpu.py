@@ -516,3 +516,37 @@ def test_repeated_calls_bit_identical(torch_mod, dev, backend):
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+
+
+@pytest.mark.parametrize("backend", ["bf16", "i8qk"])
+def test_more_segments_than_one_launch_takes(torch_mod, dev, backend):
+    """21 ragged segments, every third a view at a nonzero tile row of its
+    slot: more than one launch takes, so the oldest are merged into one
+    temporary slot; the call still matches attention over all the keys."""
+    torch = torch_mod
+    from taomate_hd_amd import KVSlot, SlotView, segment_attention
+    from taomate_hd_amd._native import MAX_SEGMENTS
+
+    heads, dim, lq = 3, 128, 200
+    sizes = [1, 17, 64, 65, 130, 3, 700, 40, 2, 96, 33, 64, 5, 128, 90, 7, 11, 300, 19, 64, 23]
+    assert len(sizes) > MAX_SEGMENTS
+    n = sum(sizes)
+    q = randn_bf16((lq, heads, dim), 301)
+    k = randn_bf16((n, heads, dim), 302, offset=key_offset(heads, dim, 303))
+    v = randn_bf16((n, heads, dim), 304)
+    kd, vd = to_dev(k, dev), to_dev(v, dev)
+    views, row = [], 0
+    for i, c in enumerate(sizes):
+        dst = 64 * (1 + i % 2) if i % 3 == 1 else 0
+        s = KVSlot(torch, heads=heads, head_dim=dim, capacity=dst + c, device=dev)
+        s.pack(kd, vd, row0=row, count=c, dst=dst)
+        views.append(SlotView(s, c, dst))
+        row += c
+    got = bf16.from_torch(segment_attention(torch, to_dev(q, dev), views, scale=dim ** -0.5, backend=backend))
+    torch.cuda.synchronize()
+    want = oatt.attention_fp64(q, k, v, dim ** -0.5)
+    if backend == "bf16":
+        mx, mean = err_stats(got, want)
+        assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+    else:
+        assert oatt.cosine(got, want) >= I8_COSINE
