@@ -10,68 +10,74 @@ namespace {
 constexpr int kTile = 64;
 
 // ---------------------------------------------------------------------------
-// tmhd_kv_pack: one workgroup = 64 slot positions of one head.
+// tmhd_kv_pack: one workgroup = 64 slot positions of one head, D threads.
 // Position p of the slot is: data row (p - dst) if dst <= p < dst + n,
 // zero if dst + n <= p < zero_to, untouched otherwise.
 // WITH_K false: the key rows of data positions are left to the caller (the
 // staged norm + RoPE kernel writes them); zero positions are still cleared.
+// Thread (dc, g) owns the 16-byte column chunk dc (columns 8 dc .. 8 dc + 7) of
+// the 8 tokens stored at transposed positions 8 g .. 8 g + 7: it loads their 8
+// key and value chunks, copies the keys, and transposes the 8 x 8 block of
+// values in registers into 8 transposed rows of 8 positions. A wave's loads
+// and stores are whole 128-byte lines; no LDS and no barrier.
 template <int D, bool WITH_K = true>
-__global__ void __launch_bounds__(256) kv_pack_kernel(const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
-                                                      int64_t ts, int64_t hs, const int32_t *__restrict__ rows,
-                                                      int32_t row0, int32_t n, uint16_t *__restrict__ ks,
-                                                      uint16_t *__restrict__ vts, int64_t khs, int64_t vhs, int32_t vrs,
-                                                      int32_t dst, int32_t zero_to, int32_t p_begin) {
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  __shared__ uint16_t tile[kTile][D + 2];
+__global__ void __launch_bounds__(D) kv_pack_kernel(const uint16_t *__restrict__ k, const uint16_t *__restrict__ v,
+                                                    int64_t ts, int64_t hs, const int32_t *__restrict__ rows,
+                                                    int32_t row0, int32_t n, uint16_t *__restrict__ ks,
+                                                    uint16_t *__restrict__ vts, int64_t khs, int64_t vhs, int32_t vrs,
+                                                    int32_t dst, int32_t zero_to, int32_t p_begin) {
   const int h = blockIdx.y;
   const int p0 = p_begin + blockIdx.x * kTile;
-  const int tid = threadIdx.x;
-  auto cls = [&](int p) -> int {  // 0 untouched, 1 data, 2 zero
-    if (p >= dst && p < dst + n) return 1;
-    if (p >= dst + n && p < zero_to) return 2;
-    return 0;
-  };
-  // keys: direct row copies; values: staged in LDS for the transpose
-  for (int c = tid; c < kTile * CPR; c += 256) {
-    const int r = c / CPR, ch = c % CPR, p = p0 + r;
-    const int kind = cls(p);
-    i32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-    if (kind == 1) {
-      const int i = p - dst;
-      const int64_t src = (int64_t)(rows ? rows[i] : row0 + i) * ts + (int64_t)h * hs + ch * 8;
-      if constexpr (WITH_K) kv = *(const i32x4 *)(k + src);
-      vv = *(const i32x4 *)(v + src);
-    }
-    if (WITH_K ? kind != 0 : kind == 2) *(i32x4 *)(ks + (int64_t)h * khs + (int64_t)p * D + ch * 8) = kv;
-    const uint32_t *vw = (const uint32_t *)&vv;
+  const int dc = threadIdx.x >> 3, g = threadIdx.x & 7;
+  int tok[8], kind[8];  // kind: 0 untouched, 1 data, 2 zero
+  bool all = true, any = false;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      tile[r][ch * 8 + 2 * e] = (uint16_t)(vw[e] & 0xffffu);
-      tile[r][ch * 8 + 2 * e + 1] = (uint16_t)(vw[e] >> 16);
-    }
+  for (int e = 0; e < 8; ++e) {
+    tok[e] = vt_position(g * 8 + e);
+    const int p = p0 + tok[e];
+    kind[e] = (p >= dst && p < dst + n) ? 1 : (p >= dst + n && p < zero_to) ? 2 : 0;
+    all = all && kind[e] != 0;
+    any = any || kind[e] != 0;
   }
-  __syncthreads();
-  // transposed values: D rows of 64 positions = 8 chunks of 8 positions each
-  for (int c = tid; c < D * 8; c += 256) {
-    const int d = c >> 3, ch = c & 7;
-    uint16_t vals[8];
-    int nwrite = 0;
+  i32x4 kv[8], vv[8];
+  if (n > 0) {
+    // every load issued before any is used: indices are clamped into the
+    // data rows and the values of other positions are dropped afterwards
+    int64_t src[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int tok = vt_position(ch * 8 + e);  // token held at this stored position
-      vals[e] = tile[tok][d];
-      nwrite += cls(p0 + tok) != 0;
+      const int i = min(max(p0 + tok[e] - dst, 0), n - 1);
+      src[e] = (int64_t)(rows ? rows[i] : row0 + i) * ts + (int64_t)h * hs + dc * 8;
     }
-    uint16_t *out = vts + (int64_t)h * vhs + (int64_t)d * vrs + p0 + ch * 8;
-    if (nwrite == 8) {
-      i32x4 pk;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) pk[e] = (int)((uint32_t)vals[2 * e] | ((uint32_t)vals[2 * e + 1] << 16));
-      *(i32x4 *)out = pk;
-    } else if (nwrite > 0) {
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (WITH_K) kv[e] = *(const i32x4 *)(k + src[e]);
+      vv[e] = *(const i32x4 *)(v + src[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (n == 0 || kind[e] != 1) kv[e] = vv[e] = i32x4{0, 0, 0, 0};
+  uint16_t *kout = ks + (int64_t)h * khs + dc * 8;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    if (WITH_K ? kind[e] != 0 : kind[e] == 2) *(i32x4 *)(kout + (int64_t)(p0 + tok[e]) * D) = kv[e];
+  if (!any) return;
+  uint16_t *out = vts + (int64_t)h * vhs + (int64_t)(dc * 8) * vrs + p0 + g * 8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    i32x4 w;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t x = (uint32_t)vv[2 * m][j >> 1], y = (uint32_t)vv[2 * m + 1][j >> 1];
+      w[m] = (int)((j & 1) ? (x >> 16) | (y & 0xffff0000u) : (x & 0xffffu) | (y << 16));
+    }
+    if (all) {
+      *(i32x4 *)(out + (int64_t)j * vrs) = w;
+    } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (cls(p0 + vt_position(ch * 8 + e)) != 0) out[e] = vals[e];
+        if (kind[e] != 0) out[(int64_t)j * vrs + e] = (uint16_t)((uint32_t)w[e >> 1] >> (16 * (e & 1)));
     }
   }
 }
@@ -377,7 +383,7 @@ int kv_pack(const void *k, const void *v, int64_t token_stride, int64_t head_str
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((p_end - p_begin) / kTile, heads);
 #define TMHD_PACK(DIM, WK)                                                                                      \
-  hipLaunchKernelGGL((kv_pack_kernel<DIM, WK>), grid, dim3(256), 0, s, (const uint16_t *)k, (const uint16_t *)v, \
+  hipLaunchKernelGGL((kv_pack_kernel<DIM, WK>), grid, dim3(DIM), 0, s, (const uint16_t *)k, (const uint16_t *)v, \
                      token_stride, head_stride, rows, row0, n, (uint16_t *)k_slot, (uint16_t *)vt_slot,          \
                      k_head_stride, vt_head_stride, vt_row_stride, dst, zero_to, p_begin)
   if (head_dim == 128 && with_k)

@@ -69,6 +69,48 @@ def test_pack_roundtrip_and_padding(torch_mod, dev):
     assert np.array_equal(bf16.from_torch(value), v[100:150])
 
 
+@pytest.mark.parametrize(
+    "D,dst,n,zero_to,use_rows",
+    [(128, 70, 50, 200, True), (128, 0, 150, 150, False), (64, 3, 61, 64, False), (64, 100, 0, 190, True),
+     (128, 130, 1, 131, False), (128, 64, 64, 0, True)],
+)
+def test_pack_through_the_c_abi_every_position(torch_mod, dev, D, dst, n, zero_to, use_rows):
+    """tmhd_kv_pack through the C ABI with unaligned ``dst`` and ``zero_to``:
+    every slot position of K and of the transposed V is the data row, zero or
+    the slot's earlier contents, as the position's class says (positions
+    dst .. dst + n data, then zeros up to zero_to, the rest untouched)."""
+    torch = torch_mod
+    from taomate_hd_amd import _native, vt_position
+
+    H, T, cap = 3, 160, 256
+    k = randn_bf16((T, H, D), 11 + D)
+    v = randn_bf16((T, H, D), 12 + D)
+    sel = np.random.default_rng(n + dst).integers(0, T, size=n).astype(np.int32) if use_rows else np.arange(5, 5 + n)
+    kd, vd = to_dev(k, dev), to_dev(v, dev)
+    rows = torch.tensor(sel, dtype=torch.int32, device=dev) if use_rows else None
+    gen = torch.Generator(device=dev).manual_seed(3)
+    ks = torch.randn((H, cap, D), generator=gen, device=dev).to(torch.bfloat16)
+    vts = torch.randn((H, D, cap), generator=gen, device=dev).to(torch.bfloat16)
+    k0, v0 = bf16.from_torch(ks), bf16.from_torch(vts)
+    lib = _native.load()
+    st = lib.tmhd_kv_pack(_native.ptr(kd), _native.ptr(vd), kd.stride(0), kd.stride(1),
+                          _native.ptr(rows) if use_rows and n else None, 5, n, _native.ptr(ks), _native.ptr(vts),
+                          cap * D, cap * D, cap, dst, zero_to, H, D, _native.stream_ptr(torch, dev))
+    _native.check(st, "tmhd_kv_pack")
+    torch.cuda.synchronize()
+    want_k, want_vt = k0.copy(), v0.copy()
+    for p in range(cap):
+        if dst <= p < dst + n:
+            want_k[:, p, :] = k[sel[p - dst]]
+        elif dst + n <= p < zero_to:
+            want_k[:, p, :] = 0
+        else:
+            continue
+        want_vt[:, :, (p // 64) * 64 + vt_position(p % 64)] = want_k[:, p, :] if p >= dst + n else v[sel[p - dst]]
+    assert np.array_equal(bf16.from_torch(ks).view(np.uint16), want_k.view(np.uint16))
+    assert np.array_equal(bf16.from_torch(vts).view(np.uint16), want_vt.view(np.uint16))
+
+
 ATTN_CASES = [
     # heads, dim, lq, segment token counts
     (8, 64, 256, [768, 256]),  # plumbing config: 768 history + 256 self
