@@ -6,6 +6,8 @@ move the running softmax reference, both backends, split last round on and off.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -15,7 +17,9 @@ from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 48
+# a wider sweep: TMHD_SWEEP_CASES=480 TMHD_SWEEP_SEED=<another base> pytest tests/test_attention_sweep_gpu.py
+N_CASES = int(os.environ.get("TMHD_SWEEP_CASES", "48"))
+SEED0 = int(os.environ.get("TMHD_SWEEP_SEED", "4242"))
 
 
 def _case(rng: np.random.Generator, c: int) -> dict:
@@ -25,10 +29,11 @@ def _case(rng: np.random.Generator, c: int) -> dict:
     splits = [int(rng.choice([int(rng.integers(1, 70)), int(rng.integers(64, 1300))])) for _ in range(int(rng.integers(1, 7)))]
     backend = str(rng.choice(["bf16", "i8qk"]))
     return dict(heads=heads, dim=dim, lq=lq, splits=splits, backend=backend, split=bool(rng.integers(0, 2)),
-                peaky=bool(rng.random() < 0.3), rows=bool(rng.random() < 0.3) and backend == "bf16", seed=2000 + 10 * c)
+                peaky=bool(rng.random() < 0.3), rows=bool(rng.random() < 0.3) and backend == "bf16",
+                seed=2000 + 10 * c + 1000 * (SEED0 - 4242))
 
 
-CASES = [_case(np.random.default_rng(4242 + c), c) for c in range(N_CASES)]
+CASES = [_case(np.random.default_rng(SEED0 + c), c) for c in range(N_CASES)]
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"{c['backend']}-H{c['heads']}-D{c['dim']}-lq{c['lq']}-s{len(c['splits'])}"
