@@ -9,6 +9,8 @@ without bias.
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -18,14 +20,16 @@ from tests.helpers import randn_bf16, to_dev
 
 pytestmark = pytest.mark.gpu
 
-N_CASES = 24
+# a wider sweep: TMHD_SWEEP_CASES=<cases> TMHD_SWEEP_SEED=<another base>
+N_CASES = int(os.environ.get("TMHD_SWEEP_CASES", "24"))
+SEED0 = int(os.environ.get("TMHD_SWEEP_SEED", "777"))
 
 
 def _case(c: int) -> dict:
-    rng = np.random.default_rng(777 + c)
+    rng = np.random.default_rng(SEED0 + c)
     return dict(m=int(rng.integers(1, 400)), n=int(rng.integers(1, 520)), k=64 * int(rng.integers(1, 21)),
                 apad=16 * int(rng.integers(0, 3)), bpad=16 * int(rng.integers(0, 3)), opad=int(rng.integers(0, 10)),
-                bias=bool(rng.integers(0, 2)), seed=5000 + c)
+                bias=bool(rng.integers(0, 2)), seed=5000 + c + 1000 * (SEED0 - 777))
 
 
 CASES = [_case(c) for c in range(N_CASES)]

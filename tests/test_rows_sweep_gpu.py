@@ -6,6 +6,8 @@ position tables, eps)."""
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -15,8 +17,11 @@ from oracle import rope as orope
 
 pytestmark = pytest.mark.gpu
 
-ROW_CASES = [777 + c for c in range(20)]
-ROPE_CASES = [4040 + c for c in range(16)]
+# a wider sweep: TMHD_SWEEP_CASES=<cases> TMHD_SWEEP_SEED=<seed offset>
+_N = os.environ.get("TMHD_SWEEP_CASES")
+_OFF = int(os.environ.get("TMHD_SWEEP_SEED", "0"))
+ROW_CASES = [777 + _OFF + c for c in range(int(_N or 20))]
+ROPE_CASES = [4040 + _OFF + c for c in range(int(_N or 16))]
 
 
 def _bf(rng, shape, std=1.0, mean=0.0):

@@ -10,6 +10,8 @@ backends."""
 
 from __future__ import annotations
 
+import os
+
 import numpy as np
 import pytest
 
@@ -20,7 +22,9 @@ from tests.helpers import err_stats, key_offset, randn_bf16, to_dev
 
 pytestmark = pytest.mark.gpu
 
-N_STREAMS = 8
+# a wider sweep: TMHD_SWEEP_CASES=<streams> TMHD_SWEEP_SEED=<another base>
+N_STREAMS = int(os.environ.get("TMHD_SWEEP_CASES", "8"))
+SEED0 = int(os.environ.get("TMHD_SWEEP_SEED", "31000"))
 
 
 def _layout(rng: np.random.Generator):
@@ -49,7 +53,7 @@ def _layout(rng: np.random.Generator):
     return np.concatenate(tags), np.concatenate(mask), tuple(bounds), live
 
 
-STREAMS = [dict(seed=31000 + 97 * s, backend=("sdpa", "sage_attn")[s % 2]) for s in range(N_STREAMS)]
+STREAMS = [dict(seed=SEED0 + 97 * s, backend=("sdpa", "sage_attn")[s % 2]) for s in range(N_STREAMS)]
 
 
 @pytest.mark.parametrize("stream", STREAMS, ids=[f"{s['backend']}-{s['seed']}" for s in STREAMS])
