@@ -673,6 +673,12 @@ def main() -> int:
             "components_ms": c2_comps,
             "shape": f"H {H}, D {D}, Lq {LQ_480} over Lkv {LKV_480} = anchor {ANCHOR_480} + 2 x {LQ_480} history "
                      f"(cache slots) + {LQ_480} self (packed per call)",
+            "roofline": roofline(
+                c2_flops / (c2_attn_ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "mfma", "TFLOP/s",
+                "attn_fwd_bf16_480p_pmc.txt", ATTN_SOURCE,
+                kernel="attn_fwd_kernel<128, bf16> (+ attn_merge_kernel<128> when the last round is split)",
+                flops_per_launch=c2_flops, kernel_ms=round(c2_attn_ms, 4),
+                timing="HIP events around each attention call on its launch stream, timed steps only"),
         }
         _log(f"bf16 480p: {c2_ms:.3f} ms per layer call, kernel {c2_attn_ms:.3f} ms")
         if result["value"] is None:

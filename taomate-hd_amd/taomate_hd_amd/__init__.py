@@ -48,6 +48,7 @@ from .quant import (
     dynamic_scaled_int8_quant,
     int8_mm_i32,
     quantize_weight,
+    quantize_weight_into,
     scaled_int8_quant,
 )
 from .session import H3StreamingSession, StreamingInferencePolicy, StreamingSession, apply_cross_chunk_cache_policy
@@ -57,11 +58,16 @@ from .w8a8 import (
     W8A8Workspace,
     cutlass_w8a8_linear,
     cutlass_w8a8_linear_swiglu,
+    enable_h3_cutlass_w8a8_workspace_,
     interleave_swiglu_rows,
     linear,
+    load_cutlass_w8a8_stream_weight_,
+    prepare_cutlass_w8a8_stream_load_slot_,
     quantize_cutlass_w8a8_swiglu_weight,
     quantize_cutlass_w8a8_weight,
+    quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_,
     register_torch_ops,
+    require_vllm_cutlass_w8a8,
     resolve_h3_cutlass_w8a8_policy,
 )
 
@@ -105,15 +111,21 @@ __all__ = [
     "cutlass_w8a8_linear_swiglu",
     "interleave_swiglu_rows",
     "dynamic_scaled_int8_quant",
+    "enable_h3_cutlass_w8a8_workspace_",
     "int8_mm_i32",
     "kv_contract_from_model",
     "linear",
+    "load_cutlass_w8a8_stream_weight_",
     "native_stream_attention_hook",
     "native_stream_attention_metadata",
     "quantize_cutlass_w8a8_swiglu_weight",
+    "prepare_cutlass_w8a8_stream_load_slot_",
     "quantize_cutlass_w8a8_weight",
+    "quantize_h3_interior_qkv_fc1_linears_cutlass_w8a8_",
     "quantize_weight",
+    "quantize_weight_into",
     "register_torch_ops",
+    "require_vllm_cutlass_w8a8",
     "resolve_h3_cutlass_w8a8_policy",
     "scaled_int8_quant",
     "segment_attention",

@@ -79,17 +79,33 @@ def quantize_weight(weight: Any) -> tuple[Any, Any]:
     """
     torch = _torch()
     _check_rows(torch, weight, "weight")
+    n, k = int(weight.shape[0]), int(weight.shape[1])
+    q = torch.empty((n, k), dtype=torch.int8, device=weight.device)
+    s = torch.empty((n, 1), dtype=torch.float32, device=weight.device)
+    quantize_weight_into(q, s, weight)
+    return q, s
+
+
+def quantize_weight_into(q: Any, scale: Any, weight: Any) -> None:
+    """``quantize_weight`` writing into caller storage: ``q`` a contiguous int8
+    ``[N, K]`` tensor (for instance rows ``start:stop`` of a prepared weight),
+    ``scale`` N contiguous fp32 values.  Rows are independent, so quantizing a
+    matrix in row ranges gives the bits of quantizing it whole."""
+    torch = _torch()
+    _check_rows(torch, weight, "weight")
+    _native.require_same_gpu(torch, weight.device, q=q, scale=scale)
     if weight.dtype != torch.bfloat16:
         raise ValueError("weight must be bf16")
     w = weight.contiguous()
     n, k = int(w.shape[0]), int(w.shape[1])
-    q = torch.empty((n, k), dtype=torch.int8, device=w.device)
-    s = torch.empty((n, 1), dtype=torch.float32, device=w.device)
+    if q.dtype != torch.int8 or tuple(q.shape) != (n, k) or not q.is_contiguous():
+        raise ValueError("q must be a contiguous int8 tensor shaped like weight")
+    if scale.dtype != torch.float32 or scale.numel() != n or not scale.is_contiguous():
+        raise ValueError("scale must be a contiguous fp32 tensor with one entry per weight row")
     status = _native.load().tmhd_weight_quant_i8(
-        _native.ptr(q), _native.ptr(s), _native.ptr(w), n, k, _native.stream_ptr(torch, w.device)
+        _native.ptr(q), _native.ptr(scale), _native.ptr(w), n, k, _native.stream_ptr(torch, w.device)
     )
     _native.check(status, "tmhd_weight_quant_i8")
-    return q, s
 
 
 def _gemm_operands(torch: Any, a: Any, b: Any) -> tuple[int, int, int, int, int]:
@@ -200,6 +216,16 @@ def cutlass_scaled_mm_swiglu(a: Any, b: Any, scale_a: Any, scale_b: Any, bias: A
             raise ValueError("bias must be a bf16 vector of N values")
         bias = bias.contiguous()
         bias_ptr = _native.ptr(bias)
+    if k % 128 == 64 and n % 256 == 0:
+        # the fused kernel takes k in 128-byte blocks; for an odd multiple of 64
+        # the projection runs on the GEMM that takes it, then its interleaved
+        # 128-column gate / up blocks are paired by fused_swiglu: the same
+        # projection values and the same SwiGLU, so the same bits
+        from .adaln import fused_swiglu
+
+        proj = torch.empty((m, n), dtype=torch.bfloat16, device=a.device)
+        cutlass_scaled_mm_out(proj, a, b, sa, sb, bias)
+        return fused_swiglu(proj.view(m, n // 256, 2, 128).transpose(1, 2).reshape(m, n))
     out = torch.empty((m, n // 2), dtype=torch.bfloat16, device=a.device)
     ws, ws_bytes = _split_workspace(torch, a.device, m, n, k)
     status = _native.load().tmhd_gemm_w8a8_swiglu_ws(

@@ -82,6 +82,8 @@ class KVSlot:
         self.k = torch.empty((self.heads, self.capacity, self.head_dim), dtype=torch.bfloat16, device=self.device)
         self.vt = torch.empty((self.heads, self.head_dim, self.capacity), dtype=torch.bfloat16, device=self.device)
         self.tokens = 0
+        # handle of the stream a pool last took this slot back on
+        self.released_on: int | None = None
         # exact fixed-point key sums of views of this slot, (row0, tokens, stream) ->
         # int64 [H, D]; dropped whenever the slot is written (pack, staged norm + RoPE)
         self.key_sums: dict[tuple[int, int, int], Any] = {}
@@ -160,6 +162,13 @@ class SlotPool:
     ``release`` takes it back.  At most ``max_free`` slots are kept free:
     beyond that the smallest free slot is returned to the allocator, so a
     pool's idle memory stays bounded (``free_bytes``).
+
+    Streams: a slot is handed out again only on the stream it was released
+    on, where the kernels that last read it are queued ahead of any new
+    writer; and ``release`` records that stream on the slot's memory, so a
+    slot returned to the allocator is not reused on its allocation stream
+    before those kernels end.  A slot in use (between ``acquire`` and
+    ``release``) is the caller's to order across streams.
     """
 
     def __init__(self, torch: Any, *, heads: int, head_dim: int, device: Any, max_free: int = 8) -> None:
@@ -178,8 +187,11 @@ class SlotPool:
 
     def acquire(self, tokens: int) -> KVSlot:
         need = round_up(max(int(tokens), 1), KV_TILE)
+        stream = self._stream_key()
         best = None
         for slot in self._free:
+            if slot.released_on != stream:
+                continue
             if slot.capacity >= need and (best is None or slot.capacity < best.capacity):
                 best = slot
         if best is not None:
@@ -188,8 +200,21 @@ class SlotPool:
             return best
         return KVSlot(self._torch, heads=self.heads, head_dim=self.head_dim, capacity=need, device=self.device)
 
+    def _stream_key(self) -> int:
+        """Handle of the current stream on the pool's device (0 off the GPU)."""
+        torch = self._torch
+        if torch.device(self.device).type != "cuda":
+            return 0
+        return int(torch.cuda.current_stream(device=self.device).cuda_stream)
+
     def release(self, slot: KVSlot) -> None:
         slot.tokens = 0
+        torch = self._torch
+        if slot.k.is_cuda:
+            stream = torch.cuda.current_stream(device=slot.k.device)
+            slot.k.record_stream(stream)
+            slot.vt.record_stream(stream)
+        slot.released_on = self._stream_key()
         self._free.append(slot)
         if len(self._free) > self.max_free:
             self._free.remove(min(self._free, key=lambda s: s.capacity))

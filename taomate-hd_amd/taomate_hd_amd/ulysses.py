@@ -100,14 +100,16 @@ def qkv_receive_layout(received: Any, out: Any | None = None) -> Any:
     ``outputs.movedim(0, 1).contiguous()``, ulysses.py:209-211, row-merged)."""
     import torch
 
-    _native.require_device_tensor(torch, received, "received")
-    if received.ndim != 5 or int(received.shape[1]) != 3 or not received.is_contiguous():
-        raise ValueError("received QKV must be a contiguous [world, 3, tokens, local_heads, head_dim] buffer")
+    if (received.ndim != 5 or int(received.shape[1]) != 3 or not received.is_contiguous()
+            or received.dtype != torch.bfloat16):
+        raise ValueError("received QKV must be a contiguous bf16 [world, 3, tokens, local_heads, head_dim] buffer")
     world, _, tokens, local, head_dim = (int(v) for v in received.shape)
     if out is None:
         out = torch.empty((world * tokens, 3 * local * head_dim), dtype=received.dtype, device=received.device)
-    elif tuple(out.shape) != (world * tokens, 3 * local * head_dim) or out.stride(1) != 1:
-        raise ValueError("out must be a [world * tokens, 3 * local_heads * head_dim] view with unit column stride")
+    elif (tuple(out.shape) != (world * tokens, 3 * local * head_dim) or out.stride(1) != 1
+            or out.dtype != torch.bfloat16):
+        raise ValueError("out must be a bf16 [world * tokens, 3 * local_heads * head_dim] view with unit column stride")
+    _native.require_device_tensor(torch, received, "received")
     _native.require_same_gpu(torch, received.device, out=out)
     lib = _native.load()
     _native.check(lib.tmhd_ulysses_qkv_receive(_native.ptr(received), tokens, local, head_dim, world,
@@ -131,7 +133,6 @@ def attention_receive_layout(value: Any, *, num_heads: int, out: Any | None = No
     (ulysses_layout.py:59-67); ``out`` may be any token-major view."""
     import torch
 
-    _native.require_device_tensor(torch, value, "value")
     if value.ndim != 4 or not value.is_contiguous() or value.dtype != torch.bfloat16:
         raise ValueError("received attention output must be a contiguous bf16 [world, tokens, local_heads, dim]")
     world, tokens, local, dim = (int(v) for v in value.shape)
@@ -139,8 +140,9 @@ def attention_receive_layout(value: Any, *, num_heads: int, out: Any | None = No
         raise ValueError(f"{num_heads} heads over {world} ranks do not give {local} local heads")
     if out is None:
         out = torch.empty((tokens, int(num_heads), dim), dtype=value.dtype, device=value.device)
-    elif tuple(out.shape) != (tokens, int(num_heads), dim) or out.stride(2) != 1:
-        raise ValueError("out must be a [tokens, heads, dim] view with unit dim stride")
+    elif tuple(out.shape) != (tokens, int(num_heads), dim) or out.stride(2) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be a bf16 [tokens, heads, dim] view with unit dim stride")
+    _native.require_device_tensor(torch, value, "value")
     _native.require_same_gpu(torch, value.device, out=out)
     lib = _native.load()
     _native.check(lib.tmhd_ulysses_attention_receive(_native.ptr(value), tokens, int(num_heads), dim, world,

@@ -8,7 +8,7 @@ from __future__ import annotations
 import pytest
 
 from tests.helpers import key_offset, randn_bf16, to_dev
-from tests.test_zz_no_alloc import _args
+from tests.test_zz_no_alloc import _args, heads_for_a_split_round, split_parts
 
 pytestmark = pytest.mark.gpu
 
@@ -18,8 +18,11 @@ def test_noalloc_attention_replays_in_a_graph(torch_mod, dev):
     from taomate_hd_amd import KVSlot, _native
 
     lib = _native.load()
-    heads, dim, lq, splits = 40, 128, 1792, [1000, 1560]  # 280 items: the split last round runs
+    cus = int(torch.cuda.get_device_properties(dev).multi_processor_count)
+    dim, lq, splits = 128, 1792, [1000, 1560]
+    heads = heads_for_a_split_round(cus, 7)  # the last round is split, so the static scratch is used
     n = sum(splits)
+    assert split_parts(heads * 7, cus, (n + 63) // 64) > 1
     kd = to_dev(randn_bf16((n, heads, dim), 91, offset=key_offset(heads, dim, 93)), dev)
     vd = to_dev(randn_bf16((n, heads, dim), 92), dev)
     views, off = [], 0

@@ -393,6 +393,11 @@ def test_slot_pool_keeps_at_most_max_free_slots_without_gpu():
     assert len(pool._free) == 2 and sorted(s.capacity for s in pool._free) == [192, 256]
     assert pool.free_bytes == sum(s.nbytes for s in pool._free)
     assert pool.acquire(100) is slots[2]  # smallest free slot that fits
+    # a slot goes back out only on the stream it was released on
+    pool.release(slots[2])
+    slots[2].released_on = 12345  # as if released on another stream
+    other = pool.acquire(100)
+    assert other is not slots[2] and other.capacity == 256  # the other free slot, released here
 
 
 def test_row_lists_are_range_checked_before_the_int32_cast_without_gpu():
@@ -415,3 +420,73 @@ def test_vt_columns_match_vt_position():
 
     for n in (0, 1, 15, 16, 17, 63, 64, 65, 1000):
         assert vt_columns(torch, n, "cpu").tolist() == [vt_position(t) for t in range(n)], n
+
+
+def test_ulysses_receive_layouts_refuse_non_bf16_buffers_without_gpu():
+    """The receive kernels address their buffers as bf16 elements: a 1-byte
+    ``out`` would be written past its end, a 4-byte one scrambled, so every
+    buffer's dtype is checked before the library is called."""
+    import torch
+
+    from taomate_hd_amd.ulysses import attention_receive_layout, qkv_receive_layout
+
+    received = torch.zeros((2, 3, 4, 2, 8), dtype=torch.bfloat16)
+    for dtype in (torch.int8, torch.uint8, torch.float32, torch.float16):
+        with pytest.raises(ValueError, match="out must be a bf16"):
+            qkv_receive_layout(received, out=torch.empty((8, 48), dtype=dtype))
+        with pytest.raises(ValueError, match="received QKV must be a contiguous bf16"):
+            qkv_receive_layout(received.to(dtype))
+    value = torch.zeros((2, 4, 3, 8), dtype=torch.bfloat16)
+    for dtype in (torch.int8, torch.float32):
+        with pytest.raises(ValueError, match="out must be a bf16"):
+            attention_receive_layout(value, num_heads=6, out=torch.empty((4, 6, 8), dtype=dtype))
+        with pytest.raises(ValueError, match="received attention output must be a contiguous bf16"):
+            attention_receive_layout(value.to(dtype), num_heads=6)
+    # correct dtypes reach the device check (no CPU path)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        qkv_receive_layout(received, out=torch.empty((8, 48), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="GPU tensor"):
+        attention_receive_layout(value, num_heads=6)
+
+
+def test_condition_resolve_binds_the_reference_runtime_module_when_importable(monkeypatch):
+    """Inside the reference runtime ``taomate_hd.model.condition_cache`` is
+    importable and the hook must consult it (the reference hook imports it,
+    attention_hook.py:322-324, 445-465); a stub module of that name stands in
+    for it here.  Injected queries still win over it, and without it the
+    package's own scope is used."""
+    import sys
+    import types
+
+    from taomate_hd_amd import condition
+
+    asked = []
+
+    def cached(layer_name, document_index):
+        asked.append(("cached", layer_name, document_index))
+        return document_index == 1
+
+    def compact(layer_name, query):
+        asked.append(("compact", layer_name))
+        return None
+
+    root, model, module = (types.ModuleType(n) for n in ("taomate_hd", "taomate_hd.model",
+                                                          "taomate_hd.model.condition_cache"))
+    root.model, model.condition_cache = model, module
+    module.condition_attention_cached, module.compact_condition_attention_output = cached, compact
+    for name, mod in (("taomate_hd", root), ("taomate_hd.model", model), ("taomate_hd.model.condition_cache", module)):
+        monkeypatch.setitem(sys.modules, name, mod)
+    assert condition.resolve() == (cached, compact)
+    cache, hook, _ = _hook_and_inputs()
+    assert hook._condition_attention_cached is cached and hook._compact_output is compact
+    assert hook._condition_attention_cached("blocks.0.attn", 1) and asked == [("cached", "blocks.0.attn", 1)]
+
+    def mine(layer_name, document_index):
+        return False
+
+    injected = type(hook)(cache, condition_attention_cached=mine)
+    assert injected._condition_attention_cached is mine and injected._compact_output is compact
+
+    monkeypatch.delitem(sys.modules, "taomate_hd.model.condition_cache")
+    monkeypatch.setitem(sys.modules, "taomate_hd.model.condition_cache", None)  # not importable
+    assert condition.resolve() == (condition.condition_attention_cached, condition.compact_condition_attention_output)

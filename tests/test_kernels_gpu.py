@@ -283,6 +283,14 @@ def test_token_quant_bit_exact(torch_mod, dev):
     wq, ws = oq.token_quant(x)
     assert np.array_equal(q.cpu().numpy(), wq)
     assert np.array_equal(s.cpu().numpy().reshape(-1), ws)
+    # rows where x * (127 / amax) and x / (amax / 127) round apart (63 vs 64):
+    # the kernel multiplies, as stated
+    from tests.test_oracle import FORM_ROWS
+
+    xf = np.zeros((2, 512), np.float32)
+    xf[:, :3] = FORM_ROWS
+    qf, _, _ = quant.scaled_int8_quant(to_dev(xf, dev))
+    assert qf.cpu().numpy()[:, :3].tolist() == [[127, 63, -63], [127, 64, -64]]
     # odd widths use the streaming variant
     x2 = randn_bf16((9, 8 * 64 * 17), 41)
     q2, s2, _ = quant.scaled_int8_quant(to_dev(x2, dev))
@@ -302,6 +310,13 @@ def test_weight_quant_bit_exact(torch_mod, dev):
     wq, wsc = oq.weight_quant(w)
     assert np.array_equal(q.cpu().numpy(), wq)
     assert np.array_equal(s.cpu().numpy().reshape(-1), wsc)
+    # the divide form of the weight quantizer (64 vs 63 where multiplying gives 63 vs 64)
+    from tests.test_oracle import FORM_ROWS
+
+    wf = np.zeros((2, 256), np.float32)
+    wf[:, :3] = FORM_ROWS
+    qf, _ = quant.quantize_weight(to_dev(wf, dev))
+    assert qf.cpu().numpy()[:, :3].tolist() == [[127, 64, -64], [127, 63, -63]]
 
 
 # k = 64 and 192 (odd multiples of 64) run the 8-wave kernel; 128 (one k block:

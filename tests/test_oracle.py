@@ -68,6 +68,32 @@ def test_token_quant_ties_round_half_even():
     assert q.tolist() == [[127, 2, -4, 0, 0, 2]] and s[0] == 1.0
 
 
+# Rows whose second value is exactly half the row maximum, so the exact
+# quotient is 63.5, a tie.  In float32 the two ways of forming it differ:
+#   row A (amax 0.4765625):  x * fl(127 / amax) = 63.499996  but  x / fl(amax / 127) = 63.5
+#   row B (amax 2.234375):   x * fl(127 / amax) = 63.5       but  x / fl(amax / 127) = 63.499996
+# so the multiply form gives (63, 64) and the divide form (64, 63): each
+# quantizer is pinned to its own stated form by these two rows.
+FORM_ROWS = np.array([[0.4765625, 0.23828125, -0.23828125], [2.234375, 1.1171875, -1.1171875]], np.float32)
+
+
+def test_token_quant_multiplies_by_127_over_amax():
+    """vLLM's per-token form, stated in include/tmhd.h: rint(x * (127 / amax))."""
+    for amax, x in FORM_ROWS[:, :2]:  # the premise: the two forms really differ here
+        mul = np.float32(x) * (np.float32(127.0) / np.float32(amax))
+        div = np.float32(x) / (np.float32(amax) / np.float32(127.0))
+        assert np.rint(mul) != np.rint(div)
+    q, s = oq.token_quant(FORM_ROWS)
+    assert q.tolist() == [[127, 63, -63], [127, 64, -64]]
+    assert s.tolist() == [np.float32(0.4765625) / np.float32(127), np.float32(2.234375) / np.float32(127)]
+
+
+def test_weight_quant_divides_by_the_scale():
+    """The reference's weight form (w8a8.py:177-178): round(W / (amax / 127))."""
+    q, s = oq.weight_quant(FORM_ROWS)
+    assert q.tolist() == [[127, 64, -64], [127, 63, -63]]
+
+
 def test_weight_quant_closed_forms():
     rng = np.random.default_rng(2)
     w = bf16.round_f32((rng.standard_normal((32, 256)) * 0.02).astype(np.float32))

@@ -28,16 +28,37 @@ def _args(torch, q, views, out, scale):
     return a
 
 
+def split_parts(items: int, cus: int, key_tiles: int) -> int:
+    """Key ranges per item of the last round, as the launch chooses them: as
+    many as fit the CUs the whole items leave free, at most 8, each at least
+    4 key tiles of 64 long; 1 = no split."""
+    rem = items % cus
+    if rem == 0:
+        return 1
+    return max(1, min(cus // rem, 8, key_tiles // 4))
+
+
+def heads_for_a_split_round(cus: int, query_tiles: int) -> int:
+    """Heads whose items (heads x query tiles) fill one round of ``cus`` CUs
+    and leave about an eighth of the next one, so that round is split."""
+    return (cus + cus // 8 + query_tiles - 1) // query_tiles
+
+
 def test_noalloc_attention_equals_workspace_entry_point(torch_mod, dev):
     torch = torch_mod
     from taomate_hd_amd import KVSlot, _native
 
     lib = _native.load()
     stream = _native.stream_ptr(torch, dev)
-    # 40 heads x 7 query tiles = 280 items: one round of 256 CUs plus 24 split items;
-    # then 5 heads x 3 tiles = 15 items, every one split, with head_dim 64
-    for heads, dim, lq, splits in ((40, 128, 1792, [1000, 1560]), (5, 64, 600, [64, 900, 3])):
+    cus = int(torch.cuda.get_device_properties(dev).multi_processor_count)
+    # one whole round of items plus a split partial one (on 256 CUs: 42 heads x 7
+    # query tiles = 294 items); then 5 heads x 3 tiles = 15 items, every one
+    # split, with head_dim 64
+    cases = ((heads_for_a_split_round(cus, 7), 128, 1792, [1000, 1560]), (5, 64, 600, [64, 900, 3]))
+    for heads, dim, lq, splits in cases:
         n = sum(splits)
+        items = heads * ((lq + 255) // 256)
+        assert split_parts(items, cus, (n + 63) // 64) > 1, (heads, lq, n, cus)  # the static scratch is used
         q = to_dev(randn_bf16((lq, heads, dim), 80 + dim), dev)
         kd = to_dev(randn_bf16((n, heads, dim), 81 + dim, offset=key_offset(heads, dim, 83)), dev)
         vd = to_dev(randn_bf16((n, heads, dim), 82 + dim), dev)
