@@ -74,9 +74,10 @@ typedef struct tmhd_attn_args {
   tmhd_kv_segment seg[TMHD_MAX_SEGMENTS];
   /*
    * Optional scratch (NULL: none).  The work is one item per (head, 256-row
-   * query tile); when the items do not fill the last round of the device's
-   * CUs, the remaining items are split into key ranges whose partial results
-   * go here and are merged by a second kernel on the same stream.  Without it
+   * query tile); when the items do not fill the last round of workgroups the
+   * device holds at once (one per CU for BF16, two per CU for INT8-QK), the
+   * remaining items are split into key ranges whose partial results go here
+   * and are merged by a second kernel on the same stream.  Without it
    * (or with fewer bytes than tmhd_attn_split_workspace_bytes) every item runs
    * whole.  Calls that share a workspace must be ordered (same stream).
    */
@@ -126,8 +127,8 @@ int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream);
 
 /*
  * Bytes of split_workspace that let every attention call with this head_dim
- * on the current device split its last round (0 for an unsupported
- * head_dim).  Has no counterpart in the reference: the reference's SDPA /
+ * on the current device split its last round, on either backend (two
+ * [256][head_dim + 1] fp32 slots per CU; 0 for an unsupported head_dim).  Has no counterpart in the reference: the reference's SDPA /
  * SageAttention calls manage their own scratch.
  */
 int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim);

@@ -252,35 +252,6 @@ __device__ __forceinline__ void qk_bf16(int qb, int hf, bool first, f32x16 &d, i
   }
 }
 #undef TMHD_QBLK
-#define TMHD_QBLK(QB, LO, HI)                                                                                      \
-  case QB:                                                                                                         \
-    if (first)                                                                                                     \
-      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q), "{v[224:239]}"(c)); \
-    else                                                                                                           \
-      asm("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(k), "{a[" #LO ":" #HI "]}"(q));                  \
-    break;
-// INT8 form: the chain starts at the accumulator vector c, in v[224:239].
-__device__ __forceinline__ void qk_i8(int qb, bool first, i32x16 &d, i32x4 k, const i32x4 &q, const i32x16 &c) {
-  switch (qb) {
-    TMHD_QBLK(0, 128, 131)
-    TMHD_QBLK(1, 132, 135)
-    TMHD_QBLK(2, 136, 139)
-    TMHD_QBLK(3, 140, 143)
-    TMHD_QBLK(4, 144, 147)
-    TMHD_QBLK(5, 148, 151)
-    TMHD_QBLK(6, 152, 155)
-    TMHD_QBLK(7, 156, 159)
-    TMHD_QBLK(8, 160, 163)
-    TMHD_QBLK(9, 164, 167)
-    TMHD_QBLK(10, 168, 171)
-    TMHD_QBLK(11, 172, 175)
-    TMHD_QBLK(12, 176, 179)
-    TMHD_QBLK(13, 180, 183)
-    TMHD_QBLK(14, 184, 187)
-    TMHD_QBLK(15, 188, 191)
-  }
-}
-#undef TMHD_QBLK
 // Output accumulator block b (16 fp32 per lane) lives in the fixed AGPRs
 // a[16b, 16b + 15] for the whole kernel: every asm that touches it names that
 // range, so the compiler never moves it, and the rare rescale can address the
@@ -331,7 +302,6 @@ __device__ __forceinline__ void npin(int hf, f32x16 &c) {
   else
     asm volatile("" : "+{v[240:255]}"(c));
 }
-__device__ __forceinline__ void npin(i32x16 &c) { asm volatile("" : "+{v[224:239]}"(c)); }
 // o *= alpha for block b, in place in its AGPRs (read, multiply, write back).
 #define TMHD_RS(N) "v_accvgpr_read_b32 %1, a" #N "\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 a" #N ", %1\n\t"
 #define TMHD_RS4(A, B, C, D) TMHD_RS(A) TMHD_RS(B) TMHD_RS(C) TMHD_RS(D)
@@ -387,14 +357,8 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 //         the current sub-tile (8 each);
 //   C(u): their bf16 pack and row-sum adds (4 each), at or after E(u) and at
 //         least one MFMA before the P.V MFMA that reads the pack;
-//   A(u): INT8 only, the row-sum adds of pair u, split from its pack: placed
-//         after the tile loads, anywhere after C(u) (for the early pairs
-//         below, in front of the score guard, so before any X unit):
-//         1-1.6% faster in a same-box A/B;
-//   M(u): INT8 dequantisation and row maximum of pair u % 8, half u / 8 of
-//         the next sub-tile's scores, after the score-read guard (costed 4
-//         for BF16, 8 for INT8: below its 12 issue cycles, which spreads the
-//         INT8 units more evenly and measured 1.5-2% faster than 12);
+//   M(u): row maximum of pair u % 8, half u / 8 of the next sub-tile's
+//         scores, after the score-read guard (costed 4);
 //   L(n): tile load n (DMA and its LDS address, 8), in the first `lwin` regions;
 //   X(u): the two exp2 of pair u of the NEXT sub-tile, for its first `nx` / 2
 //         pairs of each half (16, after the score-read guard and the pair's M
@@ -406,7 +370,7 @@ __device__ __forceinline__ void load_lds16(const void *base, uint32_t off, uint3
 // odd regions, the wait in front of each slot's first MFMA); each unit goes
 // to the cheapest region of its window (the earliest on ties).
 struct SlotPlan {
-  int e[16], c[16], m[16], l[16], x[16], a[16];
+  int e[16], c[16], m[16], l[16], x[16];
 };
 constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   int best = lo;
@@ -416,7 +380,7 @@ constexpr int plan_put(int (&cost)[64], int lo, int hi, int c) {
   return best;
 }
 constexpr int kGuardRegionOffset = 1;  // score-read guard in region 2 * nqk + 1
-constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i8, int nx) {
+constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, int nx) {
   SlotPlan s{};
   int cost[64] = {};
   const int ns = nqk + npv, nr = 2 * ns;
@@ -431,30 +395,30 @@ constexpr SlotPlan make_plan(int nqk, int npv, int db, int nld, int lwin, bool i
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * nqk + hf - 1;
       s.e[u] = early(u) ? -1 : plan_put(cost, 0, dl, 16);
-      s.c[u] = plan_put(cost, early(u) ? 0 : s.e[u], dl, i8 ? 4 : 12);
+      s.c[u] = plan_put(cost, early(u) ? 0 : s.e[u], dl, 12);
     }
   for (int q = 0; q < 8; ++q)
-    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, i8 ? 8 : 4);
+    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, 2 * nqk + 2, nr - 1, 4);
   for (int q = 4; q < 8; ++q)
     for (int hf = 0; hf < 2; ++hf) {
       const int u = hf * 8 + q, dl = 2 * (nqk + db) + hf - 1;
       s.e[u] = plan_put(cost, 0, dl, 16);
-      s.c[u] = plan_put(cost, s.e[u], dl, i8 ? 4 : 12);
+      s.c[u] = plan_put(cost, s.e[u], dl, 12);
     }
   for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, 0, lwin - 1, 8) : -1;
-  for (int u = 0; u < 16; ++u) s.a[u] = i8 ? plan_put(cost, s.c[u], early(u) ? 2 * nqk + 1 : nr - 1, 8) : -1;
   for (int u = 0; u < 16; ++u)
-    if (early(u)) s.x[u] = plan_put(cost, i8 ? s.m[u] : 2 * nqk + 2, nr - 1, 16);
+    if (early(u)) s.x[u] = plan_put(cost, 2 * nqk + 2, nr - 1, 16);
   return s;
 }
 
 // The orderings the sub-tile code relies on, checked at compile time:
-// a pair's pack after its exponentials and by its P.V deadline; maxima and
-// early exponentials after the score guard (the early ones of INT8 after
-// their pair's dequantisation); INT8 adds after the pack and, for early
-// pairs, in front of the guard (so before any X unit rewrites the carried
-// exponentials); loads inside their window.
-constexpr bool plan_valid(const SlotPlan &s, int nqk, int npv, int db, int nld, int lwin, bool i8, int nx) {
+// a pair's pack (with its row-sum adds) after its exponentials and by its
+// P.V deadline; maxima and early exponentials after the score guard; loads
+// inside their window.  An early pair's exponentials are carried into the
+// sub-tile in the registers its X unit then rewrites with the next
+// sub-tile's, so its pack and adds must precede every X unit, which the
+// deadline before the guard ensures.
+constexpr bool plan_valid(const SlotPlan &s, int nqk, int npv, int db, int nld, int lwin, int nx) {
   const int nr = 2 * (nqk + npv), guard = 2 * nqk + kGuardRegionOffset;
   for (int u = 0; u < 16; ++u) {
     const int hf = u >> 3, q = u & 7;
@@ -462,18 +426,16 @@ constexpr bool plan_valid(const SlotPlan &s, int nqk, int npv, int db, int nld, 
     const int dl = q < 4 ? 2 * nqk + hf - 1 : 2 * (nqk + db) + hf - 1;
     if (early != (s.e[u] < 0) || s.c[u] < (early ? 0 : s.e[u]) || s.c[u] > dl) return false;
     if (s.m[u] <= guard || s.m[u] >= nr) return false;
-    if (early != (s.x[u] >= 0) || (early && (s.x[u] <= guard || s.x[u] < (i8 ? s.m[u] : 0) || s.x[u] >= nr)))
-      return false;
-    if (i8 != (s.a[u] >= 0) || (i8 && (s.a[u] < s.c[u] || s.a[u] >= (early ? guard + 1 : nr)))) return false;
+    if (early != (s.x[u] >= 0) || (early && (s.x[u] <= guard || s.x[u] >= nr))) return false;
   }
   for (int n = 0; n < 16; ++n)
     if ((n < nld) != (s.l[n] >= 0) || s.l[n] >= lwin) return false;
   return true;
 }
 
-template <int D, bool I8>
+template <int D>
 __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) attn_fwd_kernel(const KArgs a) {
-  constexpr int KROW = I8 ? D : 2 * D;  // bytes per key row in memory
+  constexpr int KROW = 2 * D;  // bytes per key row in memory
   constexpr int KCPR = KROW / 16;       // 16-byte chunks per key row
   constexpr int KRS = KROW + 16;        // LDS key row stride: one pad chunk, an odd number of chunks
   constexpr int KT = kBN * KRS;         // LDS key tile bytes
@@ -484,7 +446,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   static_assert(KT % 1024 == 0 && VT % 1024 == 0, "tiles are whole wave loads");
   constexpr int KWL = (NKL + kWaves - 1) / kWaves;  // per wave (the last round is partial)
   constexpr int VWL = (NVL + kWaves - 1) / kWaves;
-  constexpr int QST = I8 ? D / 32 : D / 16;  // MFMA k-steps over head_dim
+  constexpr int QST = D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;
   constexpr int NQK = QST;     // score slots per 32-key sub-tile (one K operand, two MFMAs)
   constexpr int NPV = 2 * DB;  // output slots per sub-tile (one V operand, two MFMAs)
@@ -524,22 +486,16 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   for (int hf = 0; hf < 2; ++hf) {
     const int ql = q0 + hf * 32 + lr;
     if (ql < a.lq) {
-      if constexpr (I8) {
-        const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
+      const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
+      const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
 #pragma unroll
-        for (int st = 0; st < QST; ++st) qv[hf][st] = *(const i32x4 *)(p + st * 32);
-      } else {
-        const int row = a.q_rows ? a.q_rows[ql] : a.q_row0 + ql;
-        const uint16_t *p = a.q + (int64_t)row * a.qts + (int64_t)h * a.qhs + g * 8;
+      for (int st = 0; st < QST; ++st) {
+        const i32x4 raw = *(const i32x4 *)(p + st * 16);
 #pragma unroll
-        for (int st = 0; st < QST; ++st) {
-          const i32x4 raw = *(const i32x4 *)(p + st * 16);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t u = (uint32_t)raw[e];
-            qv[hf][st][e] =
-                (int)pack_bf16x2(__uint_as_float(u << 16) * a.c, __uint_as_float(u & 0xffff0000u) * a.c);
-          }
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t u = (uint32_t)raw[e];
+          qv[hf][st][e] =
+              (int)pack_bf16x2(__uint_as_float(u << 16) * a.c, __uint_as_float(u & 0xffff0000u) * a.c);
         }
       }
     } else {
@@ -551,13 +507,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
     for (int st = 0; st < QST; ++st) qpin(hf * QST + st, qv[hf][st]);
-  // INT8: softmax scale * log2(e) * query block scale (the wave's 64 rows lie in one 128-row block)
-  float cq = a.c;
-  if constexpr (I8) cq = a.c * a.qs[(int64_t)h * a.qshs + q0 / TMHD_QUANT_BLOCK];
-  i32x16 magic;  // INT8 score accumulator start
-#pragma unroll
-  for (int r = 0; r < 16; ++r) magic[r] = kI8Magic;
-  if constexpr (I8) npin(magic);
 
   // per-lane LDS read offsets from smem (bytes; k-step, key half, buffer and db parts are uniform/immediate)
   const uint32_t kro = lr * KRS + g * 16;
@@ -586,16 +535,15 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // load n of a tile: K blocks first (n < KWL), then V blocks
   constexpr int NLD = KWL + VWL;
   static_assert(NLD <= 16, "slot plan bounds");
-  // tile loads spread over the first NS regions (BF16: with the early exponentials in the last
-  // regions, 0.7% faster than 1.5 NS in two same-box A/Bs, 2 NS 1.3% slower) or over all of them
-  // (INT8: 1.3% faster in a same-box A/B)
+  // tile loads spread over the first NS regions (with the early exponentials in the last
+  // regions, 0.7% faster than 1.5 NS in two same-box A/Bs, 2 NS 1.3% slower)
   // early exponentials: pairs 0..3 of each query half (same-box A/B at 768p, 6 runs each, against
-  // pair 0 placed before the second E / C units: BF16 8.098 -> 7.995 ms, INT8-QK 7.314 -> 7.279 ms;
-  // pair 0 alone, placed last: 8.036 / 7.294 ms; against no early units, pair 0 gave about 1%)
+  // pair 0 placed before the second E / C units: 8.098 -> 7.995 ms; pair 0 alone, placed last:
+  // 8.036 ms; against no early units, pair 0 gave about 1%)
   constexpr int NX = 8;
-  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, I8 ? 2 * NS : NS, I8, NX);  // sub-tiles with tile loads
-  constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, I8, NX);               // sub-tiles without
-  static_assert(plan_valid(PL, NQK, NPV, DB, NLD, I8 ? 2 * NS : NS, I8, NX) && plan_valid(PN, NQK, NPV, DB, 0, 1, I8, NX),
+  constexpr SlotPlan PL = make_plan(NQK, NPV, DB, NLD, NS, NX);  // sub-tiles with tile loads
+  constexpr SlotPlan PN = make_plan(NQK, NPV, DB, 0, 1, NX);     // sub-tiles without
+  static_assert(plan_valid(PL, NQK, NPV, DB, NLD, NS, NX) && plan_valid(PN, NQK, NPV, DB, 0, 1, NX),
                 "slot plan orderings");
   // value source offsets for the V^T row stride of the current load segment
   uint32_t voff[VWL];
@@ -620,13 +568,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     for (int i = 0; i < VWL; ++i)
       load_lds16(base, (vrc[i] & 0xfffffu) * S.vrs2 + ((vrc[i] >> 20) << 4),
                  lds0 + 3 * KT + buf * VT + vblk(i) * 1024);
-  };
-  // INT8 key scale of a tile, read through the vector memory path (counted by
-  // vmcnt, so the end-of-iteration wait covers it)
-  auto load_ks = [&](const Stream &S) {
-    int idx = S.t >> 1;  // 128-token quant blocks hold two tiles
-    asm volatile("v_mov_b32 %0, %1" : "=v"(idx) : "s"(idx));
-    return S.ks[idx];
   };
   auto lds_read = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
   // valid keys of a stream's current tile (1 .. 64)
@@ -661,61 +602,39 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     }
   float lsum[2] = {0.0f, 0.0f};
   float mref[2];   // running reference of each query half (log2 units)
-  f32x16 negm[2];  // BF16: -mref in every element, the score accumulator start
+  f32x16 negm[2];  // -mref in every element, the score accumulator start
   const f32x16 zero16 = {};
 
   // ---- prologue: K(0..2), V(0..1) resident; S = scores of sub-tile 0 (minus m)
   Stream t0, t1, t2, t3;
-  stream_seek<I8>(t0, a, h, t_begin);
+  stream_seek<false>(t0, a, h, t_begin);
   t1 = t0;
-  stream_next<I8>(t1, a, h);
+  stream_next<false>(t1, a, h);
   t2 = t1;
-  stream_next<I8>(t2, a, h);
+  stream_next<false>(t2, a, h);
   t3 = t2;
-  stream_next<I8>(t3, a, h);
+  stream_next<false>(t3, a, h);
   load_k(t0, 0);
   load_k(t1, 1);
   load_v(t0, 0);
-  // valid keys and INT8 key scales of tiles j, j+1, j+2, j+3
+  // valid keys of tiles j, j+1, j+2, j+3
   int nv0 = tile_valid(t0), nv1 = tile_valid(t1), nv2 = tile_valid(t2), nv3 = tile_valid(t3);
-  float ks0 = 0.0f, ks1 = 0.0f, ks2 = 0.0f;
-  if constexpr (I8) {
-    ks0 = load_ks(t0);
-    ks1 = load_ks(t1);
-    ks2 = load_ks(t2);
-  }
   wait_vmem();
   __syncthreads();
   // scores (minus m) of the current and the next sub-tile: sub-tiles alternate
   // between the two sets, so no copies are needed
   f32x16 sA[2], sB[2];
   {
-    const float ct0 = cq * ks0;
-    if constexpr (I8) {
-      i32x16 acc[2];
 #pragma unroll
-      for (int st = 0; st < QST; ++st) {
-        const i32x4 kv = lds_read(kro + st * 32);
+    for (int st = 0; st < QST; ++st) {
+      const i32x4 kv = lds_read(kro + st * 32);
 #pragma unroll
-        for (int hf = 0; hf < 2; ++hf) qk_i8(hf * QST + st, st == 0, acc[hf], kv, qv[hf][st], magic);
+      for (int hf = 0; hf < 2; ++hf) {
+        if (st == 0) sA[hf] = zero16;
+        qk_bf16(hf * QST + st, hf, false, sA[hf], kv, qv[hf][st], zero16);
       }
-      mfma_drain();
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sA[hf][r] = fmaf(__int_as_float(acc[hf][r]), ct0, -kI8MagicF * ct0);
-    } else {
-#pragma unroll
-      for (int st = 0; st < QST; ++st) {
-        const i32x4 kv = lds_read(kro + st * 32);
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          if (st == 0) sA[hf] = zero16;
-          qk_bf16(hf * QST + st, hf, false, sA[hf], kv, qv[hf][st], zero16);
-        }
-      }
-      mfma_drain();
     }
+    mfma_drain();
     if (nv0 < 32) mask_sub(sA, nv0);
 #pragma unroll
     for (int hf = 0; hf < 2; ++hf) {
@@ -723,7 +642,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       mref[hf] = fmaxf(lm, __shfl_xor(lm, 32));
       sA[hf] -= mref[hf];
       negm[hf] = -mref[hf];
-      if constexpr (!I8) npin(hf, negm[hf]);
+      npin(hf, negm[hf]);
     }
   }
   // load streams: K of tile j+3 and V of tile j+2, issued after the barrier of iteration j
@@ -755,15 +674,14 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   //   slots [0, NQK):  scores of the next sub-tile, K rows at kb (k-step st = i);
   //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile, V chunks at vb.
   // sc: scores (minus m) of the current sub-tile; sn: receives those of the
-  // next.  nvs: valid keys of the next sub-tile (<= 0: none); ctn: INT8
-  // dequantisation of its scores; live: the next sub-tile exists.
+  // next.  nvs: valid keys of the next sub-tile (<= 0: none); live: the next
+  // sub-tile exists.
   // With loads, the slots also issue the tile loads of the iteration.  pre:
   // the operands of the first LA slots, read by the previous sub-tile; on
   // return, those of the next sub-tile (K rows at kbn).
   auto sub_tile = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], uint32_t kb, uint32_t vb, uint32_t kbn, i32x4 (&pre)[LA],
-                      int nvs, float ctn, bool live, auto loads_c, const char *lkb, uint32_t lkd, const char *lvb,
+                      int nvs, bool live, auto loads_c, const char *lkb, uint32_t lkd, const char *lvb,
                       uint32_t lvd) {
-    const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
     auto read_op = [&](int i) -> i32x4 {
       if (i < NQK) return lds_read(kb + i * 32);
       const int p = i - NQK, st = p / DB, db = p % DB;
@@ -771,7 +689,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     };
     i32x4 ops[NS];
     i32x4 pk[2][2];  // P as bf16 pairs: [query half][16-key step]
-    i32x16 sni[2];
     float ts[2] = {0.0f, 0.0f};
     float lm[2] = {-INFINITY, -INFINITY};
 #pragma unroll
@@ -811,39 +728,21 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         if (pl.c[u] == r) {
           const int hf = u >> 3, q = u & 7;
           int pr = (int)pack_bf16x2(pe[hf][q][0], pe[hf][q][1]);
-          if constexpr (!I8) {
-            ts[hf] += pe[hf][q][0];
-            ts[hf] += pe[hf][q][1];
-          }
+          ts[hf] += pe[hf][q][0];
+          ts[hf] += pe[hf][q][1];
           asm volatile("" : "+v"(pr), "+v"(ts[hf]));  // keeps the pack and the row sum in this region
           pk[hf][q >> 2][q & 3] = pr;
         }
-      if constexpr (I8)
-#pragma unroll
-        for (int u = 0; u < 16; ++u)
-          if (pl.a[u] == r) {
-            const int hf = u >> 3, q = u & 7;
-            ts[hf] += pe[hf][q][0];
-            ts[hf] += pe[hf][q][1];
-            asm volatile("" : "+v"(ts[hf]));  // keeps the row sum in this region
-          }
       if (r == 2 * NQK + kGuardRegionOffset) {
         // first reads of the next sub-tile's scores: at least 12 wait states
         // after the last score MFMA (the MFMA in front of this region and
         // these 10); naming the results keeps every read below
-        if constexpr (I8)
-          asm volatile("s_nop 10" : "+v"(sni[0]), "+v"(sni[1]));
-        else
-          asm volatile("s_nop 10" : "+v"(sn[0]), "+v"(sn[1]));
+        asm volatile("s_nop 10" : "+v"(sn[0]), "+v"(sn[1]));
       }
 #pragma unroll
       for (int u = 0; u < 16; ++u)
         if (pl.m[u] == r) {
           const int hf = u >> 3, rr = (u & 7) * 2;
-          if constexpr (I8) {
-            sn[hf][rr] = fmaf(__int_as_float(sni[hf][rr]), ctn, nbn[hf]);
-            sn[hf][rr + 1] = fmaf(__int_as_float(sni[hf][rr + 1]), ctn, nbn[hf]);
-          }
           lm[hf] = fmaxf(lm[hf], fmaxf(sn[hf][rr], sn[hf][rr + 1]));
           asm volatile("" : "+v"(lm[hf]));  // keeps the row maximum in this region
         }
@@ -857,10 +756,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         }
       __builtin_amdgcn_sched_barrier(0);
       if (i < NQK) {
-        if constexpr (I8)
-          qk_i8(hr * QST + i, i == 0, sni[hr], ops[i], qv[hr][i], magic);
-        else
-          qk_bf16(hr * QST + i, hr, i == 0, sn[hr], ops[i], qv[hr][i], negm[hr]);
+        qk_bf16(hr * QST + i, hr, i == 0, sn[hr], ops[i], qv[hr][i], negm[hr]);
       } else {
         const int p = i - NQK, st = p / DB, db = p % DB;
         // the P group read here was packed in the region in front of the previous MFMA
@@ -897,7 +793,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         mref[hf] += delta;
         early_exp(sn, hf);  // against the new reference
         negm[hf] = -mref[hf];
-        if constexpr (!I8) npin(hf, negm[hf]);
+        npin(hf, negm[hf]);
       }
       asm volatile("s_nop 2" ::: "memory");
     }
@@ -912,12 +808,12 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   set_voff(lvrs);
   for (;;) {
     // P of keys 0..31 of tile j; scores of keys 32..63 of tile j come next
-    sub_tile(sA, sB, kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true, std::true_type{}, lkb,
+    sub_tile(sA, sB, kro + b0 * KT + 32 * KRS, vro + b0 * VT, kro + b1 * KT, pre, nv0 - 32, true, std::true_type{}, lkb,
              lkd, lvb, lvd);
     // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 come next
     // (after the last tile they read a stale in-bounds buffer and are unused)
     const bool more = j + 1 < cnt;
-    sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more, std::false_type{},
+    sub_tile(sB, sA, kro + b1 * KT, vro + b0 * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, more, std::false_type{},
              lkb, lkd, lvb, lvd);
     if (!more) break;
     ++j;
@@ -926,8 +822,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     nv0 = nv1;
     nv1 = nv2;
     nv2 = nv3;
-    ks0 = ks1;
-    ks1 = ks2;
     const int bf = b0;  // buffers rotate: tile t lives in buffer t % 3
     b0 = b1;
     b1 = b2;
@@ -942,9 +836,8 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       set_voff(lvrs);
     }
     lvd = lds0 + 3 * KT + b1 * VT;
-    if constexpr (I8) ks2 = load_ks(sk);
     sv = sk;
-    stream_next<I8>(sk, a, h);
+    stream_next<false>(sk, a, h);
     nv3 = tile_valid(sk);
   }
 
@@ -965,6 +858,520 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
       const float inv = 1.0f / lt;
       const int rl = w * kQW + hf * 32 + lr;  // row within the item
+      if (q0 + hf * 32 + lr < a.lq) {
+        float *op = wo + rl * D + 4 * g;
+#pragma unroll
+        for (int db = 0; db < DB; ++db)
+#pragma unroll
+          for (int u = 0; u < 4; ++u)
+            *(f32x4 *)(op + db * 32 + 8 * u) = f32x4{o[hf][db][4 * u] * inv, o[hf][db][4 * u + 1] * inv,
+                                                     o[hf][db][4 * u + 2] * inv, o[hf][db][4 * u + 3] * inv};
+        if (g == 0) wo[kBM * D + rl] = mref[hf] + __log2f(lt);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
+    const float inv = 1.0f / lt;
+    const int ql = q0 + hf * 32 + lr;
+    if (ql < a.lq) {
+      const int row = a.o_rows ? a.o_rows[ql] : a.o_row0 + ql;
+      uint16_t *op = a.o + (int64_t)row * a.ots + (int64_t)h * a.ohs + 4 * g;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          i32x2 pr = {(int)pack_bf16x2(o[hf][db][4 * u] * inv, o[hf][db][4 * u + 1] * inv),
+                      (int)pack_bf16x2(o[hf][db][4 * u + 2] * inv, o[hf][db][4 * u + 3] * inv)};
+          *(i32x2 *)(op + db * 32 + 8 * u) = pr;
+        }
+    }
+  }
+}
+
+// ---- INT8-QK attention with two workgroups per CU (two waves per SIMD) ----
+//
+// The kernel above holds one wave per SIMD.  Issuing an MFMA blocks the
+// issuing wave for about half of the MFMA's cycles, so a lone wave slips only
+// a few VALU instructions under each MFMA; the INT8-QK sub-tile carries 24
+// MFMAs (8 INT8 Q.K^T, 16 BF16 P.V) and about 160 softmax VALU instructions,
+// more than fit, and the matrix cores idle.  A second wave on the SIMD issues
+// while the first is blocked: measured on one MI355X, a mix of 24 MFMAs and
+// 160 such VALU instructions costs 34.5 cycles per MFMA with two waves per
+// SIMD against 46.2 with one (32.0 for the MFMAs alone).  A wave then has 256
+// registers.  INT8 query operands take 32 per lane (BF16: 64), and with:
+//   * all operands and accumulators in VGPRs (a kernel that touches AGPRs
+//     gets them split 128 / 128, and the output accumulators alone fill 128);
+//   * the score chains starting at the MFMA's inline constant 0, each score
+//     converted (v_cvt_f32_i32) and dequantised with the reference folded in
+//     (one FMA);
+//   * one score buffer: the next sub-tile's scores are converted,
+//     exponentiated and packed to bf16 under the current sub-tile's P.V
+//     MFMAs, so only the packed probabilities (16 registers) are double-buffered;
+//   * two LDS operand reads in flight instead of four;
+//   * value tiles double-buffered (64.5 KiB of LDS per workgroup at head_dim
+//     128, so two workgroups fit a CU)
+// the loop fits 256 registers without spilling.  The exponentials are
+// computed before the next sub-tile's row maximum is known; a sub-tile whose
+// maximum exceeds the reference by more than 2^8 (lazy rescale), or that is
+// partial (masked keys), is recomputed in a rare branch: its scores again
+// from LDS, masked, the reference moved and O and l rescaled, then its
+// probabilities against the new reference.  The work decomposition (256 query
+// rows of one head per workgroup, 64 per wave), slot layouts, tile loads and
+// split last round are those of the kernel above.
+constexpr int kI8LA = 1;  // LDS operand reads in flight ahead of their slot
+// the probabilities of a lane's 16 keys sum to at most 16 * 2^12 while every
+// one is at most 2^12 (score at most 12 above the reference, log2 units)
+constexpr float kRowSumBound = 16.0f * 4096.0f;
+
+// Slot plan of one INT8 sub-tile.  Regions are as in make_plan; units:
+//   M(u): conversion, dequantisation and row maximum of pair u % 8 (query half
+//         u / 8) of the next sub-tile's scores (cost 20), after the score-read
+//         guard;
+//   E(u): its two exp2, in place (16), after M(u);
+//   C(u): their bf16 pack and row-sum adds (12), after E(u) and after the
+//         last P.V MFMA that reads the first pack group of the current
+//         sub-tile (the new packs reuse those registers);
+//   L(n): tile load n (8) in regions [lwlo, nr), the last ones, where the
+//         packs have freed score registers for the load offsets.
+struct SlotPlan8 {
+  int m[16], e[16], c[16], l[16];
+};
+constexpr SlotPlan8 make_plan8(int nqk, int npv, int db, int nld, int lwlo) {
+  SlotPlan8 s{};
+  int cost[64] = {};
+  const int ns = nqk + npv, nr = 2 * ns, guard = 2 * nqk + kGuardRegionOffset, cfree = 2 * (nqk + db);
+  for (int i = 0; i < ns; ++i) {
+    cost[2 * i] += 4;
+    cost[2 * i + 1] += 4;
+  }
+  cost[guard] += 11;
+  for (int n = 0; n < 16; ++n) s.l[n] = n < nld ? plan_put(cost, lwlo, nr - 1, 8) : -1;
+  for (int q = 0; q < 8; ++q)
+    for (int hf = 0; hf < 2; ++hf) s.m[hf * 8 + q] = plan_put(cost, guard + 1, nr - 1, 20);
+  for (int q = 0; q < 8; ++q)
+    for (int hf = 0; hf < 2; ++hf) s.e[hf * 8 + q] = plan_put(cost, s.m[hf * 8 + q], nr - 1, 16);
+  for (int q = 0; q < 8; ++q)
+    for (int hf = 0; hf < 2; ++hf) {
+      const int u = hf * 8 + q;
+      s.c[u] = plan_put(cost, s.e[u] > cfree ? s.e[u] : cfree, nr - 1, 12);
+    }
+  return s;
+}
+constexpr bool plan8_valid(const SlotPlan8 &s, int nqk, int npv, int db, int nld, int lwlo) {
+  const int nr = 2 * (nqk + npv), guard = 2 * nqk + kGuardRegionOffset, cfree = 2 * (nqk + db);
+  for (int u = 0; u < 16; ++u)
+    if (s.m[u] <= guard || s.e[u] < s.m[u] || s.c[u] < s.e[u] || s.c[u] < cfree || s.c[u] >= nr) return false;
+  for (int n = 0; n < 16; ++n)
+    if ((n < nld) != (s.l[n] >= 0) || (n < nld && (s.l[n] < lwlo || s.l[n] >= nr))) return false;
+  return true;
+}
+
+// S^T (+)= K Q^T for one 32-byte k-step, all in VGPRs; `first` starts the
+// chain at 0.  Volatile, like every MFMA of this kernel: the hazard waits in
+// front of VALU reads of MFMA results (mfma_drain, the score guard) are
+// volatile asm too, and only volatile asm keeps its order relative to them (a
+// plain asm MFMA may be sunk below a drain that does not name its registers).
+__device__ __forceinline__ void qk_i8z(bool first, i32x16 &d, i32x4 k, const i32x4 &q, const i32x16 &c) {
+  if (first)
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "v"(q), "v"(c));
+  else
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(k), "v"(q));
+}
+// O^T += V^T P^T with the accumulator in VGPRs (the packs are at least a
+// sub-tile old, past the 2 wait states a VALU write needs).
+__device__ __forceinline__ void pv_v(f32x16 &o, i32x4 v, i32x4 p) {
+  asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(o) : "v"(v), "v"(p));
+}
+
+template <int D>
+__global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_i8_kernel(const KArgs a) {
+  constexpr int KROW = D;            // bytes per int8 key row
+  constexpr int KCPR = KROW / 16;    // 16-byte chunks per key row
+  constexpr int KRS = KROW + 16;     // LDS key row stride (one pad chunk)
+  constexpr int KT = kBN * KRS;      // LDS key tile bytes
+  constexpr int VRS = kBN * 2 + 16;  // LDS value row stride
+  constexpr int VT = D * VRS;        // LDS value tile bytes
+  constexpr int NKL = KT / 1024;
+  constexpr int NVL = VT / 1024;
+  static_assert(KT % 1024 == 0 && VT % 1024 == 0, "tiles are whole wave loads");
+  constexpr int KWL = (NKL + kWaves - 1) / kWaves;
+  constexpr int VWL = (NVL + kWaves - 1) / kWaves;
+  constexpr int QST = D / 32;  // INT8 k-steps over head_dim
+  constexpr int DB = D / 32;
+  constexpr int NQK = QST;
+  constexpr int NPV = 2 * DB;
+  constexpr int NS = NQK + NPV;
+  constexpr int LA = kI8LA;
+  static_assert(LA <= NQK && NS <= 32 && NPV >= 4, "slot plan bounds");
+
+  // LDS: three K tiles (tile t in buffer t % 3), then two V tiles (t % 2),
+  // then each lane's tile-load source offsets (8 words per lane)
+  constexpr int TAB = 3 * KT + 2 * VT;
+  __shared__ __attribute__((aligned(1024))) char smem[TAB + kWaves * 64 * 32];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+
+  int L, part = -1, t_begin = 0, cnt = a.ntiles;
+  if ((int)blockIdx.x < a.full) {
+    L = xcd_logical_id(blockIdx.x, a.full);
+  } else {
+    const int tb = blockIdx.x - a.full, item = tb / a.nsplit;
+    L = a.full + item;
+    part = tb - item * a.nsplit;
+    t_begin = a.ntiles * part / a.nsplit;
+    cnt = a.ntiles * (part + 1) / a.nsplit - t_begin;
+  }
+  const int h = L / a.nqt;
+  const int qt = L - h * a.nqt;
+  const int tid = threadIdx.x, lane = tid & 63, lr = lane & 31, g = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int q0 = qt * kBM + w * kQW;
+
+  // query operands of both 32-row halves (B operands of S^T = K Q^T)
+  i32x4 qv[2][QST];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int ql = q0 + hf * 32 + lr;
+    const int8_t *p = a.q8 + (int64_t)h * a.q8hs + (int64_t)ql * D + g * 16;
+#pragma unroll
+    for (int st = 0; st < QST; ++st) qv[hf][st] = ql < a.lq ? *(const i32x4 *)(p + st * 32) : i32x4{0, 0, 0, 0};
+  }
+  // softmax scale * log2(e) * query block scale (the wave's 64 rows lie in one 128-row block)
+  const float cq = a.c * a.qs[(int64_t)h * a.qshs + q0 / TMHD_QUANT_BLOCK];
+
+  const uint32_t kro = lr * KRS + g * 16;
+  const uint32_t vro = 3 * KT + lr * VRS + g * 16;
+
+  // per-lane source offsets of the tile loads, kept in LDS (the registers are
+  // the loop's scarcest resource) and read at the start of each loading
+  // sub-tile: keys tile-invariant; values (row, chunk) packed, scaled by the
+  // segment's V^T row stride at the load
+  auto kblk = [&](int i) { return min(w + i * kWaves, NKL - 1); };
+  auto vblk = [&](int i) { return min(w + i * kWaves, NVL - 1); };
+  constexpr int NLD = KWL + VWL;
+  static_assert(NLD <= 8, "eight offset words per lane");
+  {
+    uint32_t tab[8] = {};
+#pragma unroll
+    for (int i = 0; i < KWL; ++i) {
+      const int c = kblk(i) * 64 + lane, row = c / (KCPR + 1), chunk = min(c - row * (KCPR + 1), KCPR - 1);
+      tab[i] = row * KROW + chunk * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < VWL; ++i) {
+      const int c = vblk(i) * 64 + lane, row = c / 9, chunk = min(c - row * 9, 7);
+      tab[KWL + i] = (uint32_t)row | ((uint32_t)chunk << 20);
+    }
+    *(i32x4 *)(smem + TAB + tid * 32) = i32x4{(int)tab[0], (int)tab[1], (int)tab[2], (int)tab[3]};
+    *(i32x4 *)(smem + TAB + tid * 32 + 16) = i32x4{(int)tab[4], (int)tab[5], (int)tab[6], (int)tab[7]};
+  }
+  auto read_tab = [&](uint32_t (&t)[8]) {
+    const i32x4 lo = *(const i32x4 *)(smem + TAB + tid * 32), hi = *(const i32x4 *)(smem + TAB + tid * 32 + 16);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      t[e] = (uint32_t)lo[e];
+      t[4 + e] = (uint32_t)hi[e];
+    }
+  };
+  auto voff = [&](uint32_t x, uint32_t vrs2) { return (x & 0xfffffu) * vrs2 + ((x >> 20) << 4); };
+  // the tile loads go into the last NLD regions (at least the last 8); their
+  // offsets are read from the table TABLEAD regions before the window
+  constexpr int LWLO = 2 * NS - (NLD > 8 ? NLD : 8);
+  constexpr int TABLEAD = 4;
+  static_assert(LWLO >= TABLEAD, "room for the offset-table read");
+  constexpr SlotPlan8 PL = make_plan8(NQK, NPV, DB, NLD, LWLO);
+  constexpr SlotPlan8 PN = make_plan8(NQK, NPV, DB, 0, LWLO);
+  static_assert(plan8_valid(PL, NQK, NPV, DB, NLD, LWLO) && plan8_valid(PN, NQK, NPV, DB, 0, LWLO),
+                "slot plan orderings");
+  auto load_one = [&](int n, const uint32_t (&t)[8], const char *kbase, uint32_t kdst, const char *vbase,
+                      uint32_t vdst, uint32_t vrs2) {
+    if (n < KWL)
+      load_lds16(kbase, t[n], kdst + kblk(n) * 1024);
+    else
+      load_lds16(vbase, voff(t[n], vrs2), vdst + vblk(n - KWL) * 1024);
+  };
+  auto load_k = [&](const uint32_t (&t)[8], const Stream &S, int buf) {
+    const char *base = S.kb + (int64_t)S.t * (kBN * KROW);
+#pragma unroll
+    for (int i = 0; i < KWL; ++i) load_lds16(base, t[i], lds0 + buf * KT + kblk(i) * 1024);
+  };
+  auto load_v = [&](const uint32_t (&t)[8], const Stream &S, int buf) {
+    const char *base = S.vb + S.t * (kBN * 2);
+#pragma unroll
+    for (int i = 0; i < VWL; ++i) load_lds16(base, voff(t[KWL + i], S.vrs2), lds0 + 3 * KT + buf * VT + vblk(i) * 1024);
+  };
+  auto load_ks = [&](const Stream &S) {
+    int idx = S.t >> 1;  // 128-token quant blocks hold two tiles
+    asm volatile("v_mov_b32 %0, %1" : "=v"(idx) : "s"(idx));
+    return S.ks[idx];
+  };
+  auto lds_read = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
+  auto tile_valid = [](const Stream &S) { return min(S.tok - S.t * kBN, kBN); };
+  f32x16 o[2][DB];
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[hf][db][r] = 0.0f;
+  float lsum[2] = {0.0f, 0.0f};
+  float mref[2] = {0.0f, 0.0f};  // running reference of each query column (log2 units)
+  i32x16 sn[2];                   // scores of the next sub-tile
+  i32x16 magic;                   // score chain start: its bits read as the float 1.5 * 2^23 + q.k
+#pragma unroll
+  for (int r = 0; r < 16; ++r) magic[r] = kI8Magic;
+  // scores live as the bits of floats in i32x16 (the MFMA writes int32
+  // accumulators, converted in place)
+  auto f = [](int bits) { return __int_as_float(bits); };
+  // the wait states in front of VALU reads of MFMA results, naming the
+  // registers read after them so that no read moves above the wait
+  auto drain_scores = [&]() { asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15" : "+v"(sn[0]), "+v"(sn[1])::"memory"); };
+  auto drain_o = [&]() {
+    mfma_drain();
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int db = 0; db < DB; ++db) asm volatile("" : "+v"(o[hf][db]));
+  };
+  auto sub_max = [&](const i32x16 &s) {
+    float m = fmaxf(f(s[0]), f(s[1]));
+#pragma unroll
+    for (int r = 2; r < 16; r += 2) m = fmaxf(m, fmaxf(f(s[r]), f(s[r + 1])));
+    return m;
+  };
+
+
+  // Rare path, and the first sub-tile: the scores of a 32-key sub-tile from
+  // LDS (K rows at kb) into sn, dequantised against the reference, keys at or
+  // beyond nvalid masked, the reference moved where a score exceeds it by
+  // more than 2^8 (O and l rescaled; `first`: set to the sub-tile's maximum),
+  // then the probabilities packed into pkn and their row sums added to l.
+  auto full_softmax = [&](uint32_t kb, int nvalid, float ct, bool first, i32x4 (&pkn)[2][2]) {
+#pragma unroll
+    for (int st = 0; st < QST; ++st) {
+      const i32x4 kv = lds_read(kb + st * 32);
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) qk_i8z(st == 0, sn[hf], kv, qv[hf][st], magic);
+    }
+    drain_scores();  // the score results, and every P.V accumulation in flight
+    const int t = nvalid - 4 * g;  // element r of a lane holds key 8 (r / 4) + 4 g + r % 4
+    float cm[2];
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float x = fmaf(f(sn[hf][r]), ct, -fmaf(kI8MagicF, ct, mref[hf]));
+        sn[hf][r] = __float_as_int(8 * (r >> 2) + (r & 3) >= t ? -INFINITY : x);
+      }
+      const float lm = sub_max(sn[hf]);
+      cm[hf] = fmaxf(lm, __shfl_xor(lm, 32));
+    }
+    if (first) {
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        mref[hf] = cm[hf];  // the wave's first keys set the reference
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sn[hf][r] = __float_as_int(f(sn[hf][r]) - cm[hf]);
+      }
+    } else if (__any(fmaxf(cm[0], cm[1]) > kLazyRescale)) {
+      drain_o();
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        const float delta = fmaxf(cm[hf], 0.0f);
+        const float alpha = __builtin_amdgcn_exp2f(-delta);
+        lsum[hf] *= alpha;
+#pragma unroll
+        for (int db = 0; db < DB; ++db) o[hf][db] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sn[hf][r] = __float_as_int(f(sn[hf][r]) - delta);
+        mref[hf] += delta;
+      }
+      asm volatile("s_nop 2" ::: "memory");  // VALU writes of O before the next accumulation
+    }
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const float e0 = __builtin_amdgcn_exp2f(f(sn[hf][2 * q])), e1 = __builtin_amdgcn_exp2f(f(sn[hf][2 * q + 1]));
+        pkn[hf][q >> 2][q & 3] = (int)pack_bf16x2(e0, e1);
+        lsum[hf] += e0;
+        lsum[hf] += e1;
+      }
+  };
+
+  // ---- prologue: K(0), K(1), V(0) resident; P of sub-tile 0
+  Stream t0, t1, t2, t3;
+  stream_seek<true>(t0, a, h, t_begin);
+  t1 = t0;
+  stream_next<true>(t1, a, h);
+  t2 = t1;
+  stream_next<true>(t2, a, h);
+  t3 = t2;
+  stream_next<true>(t3, a, h);
+  __syncthreads();  // the offset table
+  {
+    uint32_t t[8];
+    read_tab(t);
+    load_k(t, t0, 0);
+    load_k(t, t1, 1);
+    load_v(t, t0, 0);
+  }
+  int nv0 = tile_valid(t0), nv1 = tile_valid(t1), nv2 = tile_valid(t2), nv3 = tile_valid(t3);
+  float ks2 = load_ks(t2);
+  float ks0 = load_ks(t0), ks1 = load_ks(t1);
+  wait_vmem();
+  __syncthreads();
+  ks0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ks0)));
+  ks1 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ks1)));
+  i32x4 pkA[2][2], pkB[2][2];  // packed probabilities of the current / next sub-tile, alternating
+  full_softmax(kro, nv0, cq * ks0, true, pkA);
+  Stream sk = t3, sv = t2;  // K of tile j+3 and V of tile j+2, issued after the barrier of iteration j
+  i32x4 pre[LA];
+#pragma unroll
+  for (int i = 0; i < LA; ++i) pre[i] = lds_read(kro + 32 * KRS + i * 32);
+
+  int j = 0, b0 = 0, b1 = 1, b2 = 2, vb = 0;  // K buffers of tiles j, j+1, j+2; V buffer of tile j
+
+  // One 32-key sub-tile in NS slots of two MFMAs (one per query half), each
+  // MFMA fenced with the units the plan puts in front of it:
+  //   slots [0, NQK):  scores of the next sub-tile into sn, K rows at kb;
+  //   slots [NQK, NS): O^T += V^T P^T of the current sub-tile (packs pk),
+  //                    V chunks at vbo; under them the next sub-tile's
+  //                    probabilities go into pkn.
+  // Slot i issues the LDS operand read of slot i + LA; the last ones read the
+  // first operands of the sub-tile after (K rows at kbn) into pre.
+  auto sub_tile = [&](i32x4 (&pk)[2][2], i32x4 (&pkn)[2][2], uint32_t kb, uint32_t vbo, uint32_t kbn,
+                      i32x4 (&pre)[LA], int nvs, float ctn, bool live, auto loads_c, const char *lkb, uint32_t lkd,
+                      const char *lvb, uint32_t lvd, uint32_t lvrs) {
+    const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
+    auto read_op = [&](int i) -> i32x4 {
+      if (i < NQK) return lds_read(kb + i * 32);
+      const int p = i - NQK, st = p / DB, db = p % DB;
+      return lds_read(vbo + db * 32 * VRS + 2 * st * 16);
+    };
+    i32x4 ops[NS];
+    float ts[2] = {0.0f, 0.0f};
+    constexpr bool loads = decltype(loads_c)::value;
+    uint32_t tab[8];
+#pragma unroll
+    for (int i = 0; i < LA; ++i) ops[i] = pre[i];
+#pragma clang loop unroll(full)
+    for (int r = 0; r < 2 * NS; ++r) {
+      const int i = r >> 1, hr = r & 1;
+      constexpr SlotPlan8 pl = loads ? PL : PN;
+      if (hr == 1) {
+        if (i + LA < NS)
+          ops[i + LA] = read_op(i + LA);
+        else
+          pre[i + LA - NS] = lds_read(kbn + (i + LA - NS) * 32);
+      }
+      if (loads && r == LWLO - TABLEAD) read_tab(tab);
+      if (loads)
+#pragma unroll
+        for (int n = 0; n < NLD; ++n)
+          if (pl.l[n] == r) load_one(n, tab, lkb, lkd, lvb, lvd, lvrs);
+      if (r == 2 * NQK + kGuardRegionOffset) {
+        // first reads of the scores: at least 12 wait states after the last
+        // score MFMA; naming them keeps every read below
+        asm volatile("s_nop 10" : "+v"(sn[0]), "+v"(sn[1]));
+      }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.m[u] == r) {
+          const int hf = u >> 3, rr = (u & 7) * 2;
+          sn[hf][rr] = __float_as_int(fmaf(f(sn[hf][rr]), ctn, nbn[hf]));
+          sn[hf][rr + 1] = __float_as_int(fmaf(f(sn[hf][rr + 1]), ctn, nbn[hf]));
+          asm volatile("" : "+v"(sn[hf][rr]), "+v"(sn[hf][rr + 1]));
+        }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.e[u] == r) {
+          const int hf = u >> 3, q = u & 7;
+          sn[hf][2 * q] = __float_as_int(__builtin_amdgcn_exp2f(f(sn[hf][2 * q])));
+          sn[hf][2 * q + 1] = __float_as_int(__builtin_amdgcn_exp2f(f(sn[hf][2 * q + 1])));
+          asm volatile("" : "+v"(sn[hf][2 * q]), "+v"(sn[hf][2 * q + 1]));
+        }
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        if (pl.c[u] == r) {
+          const int hf = u >> 3, q = u & 7;
+          int pr = (int)pack_bf16x2(f(sn[hf][2 * q]), f(sn[hf][2 * q + 1]));
+          ts[hf] += f(sn[hf][2 * q]);
+          ts[hf] += f(sn[hf][2 * q + 1]);
+          asm volatile("" : "+v"(pr), "+v"(ts[hf]));
+          pkn[hf][q >> 2][q & 3] = pr;
+        }
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < NQK) {
+        qk_i8z(i == 0, sn[hr], ops[i], qv[hr][i], magic);
+      } else {
+        const int p = i - NQK, st = p / DB, db = p % DB;
+        pv_v(o[hr][db], ops[i], pk[hr][st]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!live) return;
+    // a lane's 16 probabilities sum to at most 16 * 2^12 unless one exceeds
+    // 2^12 (or overflowed): then, or for a partial sub-tile, recompute
+    if (nvs < 32 || __any(!(fmaxf(ts[0], ts[1]) <= kRowSumBound))) {
+      int nvo = nvs;  // opaque inside the branch: keeps the comparisons from being hoisted
+      asm volatile("" : "+s"(nvo));
+      full_softmax(kb, nvo, ctn, false, pkn);
+      return;
+    }
+    lsum[0] += ts[0];
+    lsum[1] += ts[1];
+  };
+
+  // tile loads issued from the slots of iteration j: K(j+2) and V(j+1)
+  const char *lkb = t2.kb + (int64_t)t2.t * (kBN * KROW), *lvb = t1.vb + t1.t * (kBN * 2);
+  uint32_t lvrs = t1.vrs2, lkd = lds0 + 2 * KT, lvd = lds0 + 3 * KT + 1 * VT;
+  for (;;) {
+    // P of keys 0..31 of tile j; scores of keys 32..63 of tile j
+    sub_tile(pkA, pkB, kro + b0 * KT + 32 * KRS, vro + vb * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true,
+             std::true_type{}, lkb, lkd, lvb, lvd, lvrs);
+    // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 (after the
+    // last tile they read a stale in-bounds buffer and are unused)
+    const bool more = j + 1 < cnt;
+    sub_tile(pkB, pkA, kro + b1 * KT, vro + vb * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more,
+             std::false_type{}, lkb, lkd, lvb, lvd, lvrs);
+    if (!more) break;
+    ++j;
+    wait_vmem();
+    __syncthreads();
+    nv0 = nv1;
+    nv1 = nv2;
+    nv2 = nv3;
+    ks0 = ks1;
+    ks1 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(ks2)));  // uniform: keep it in an SGPR
+    const int bf = b0;
+    b0 = b1;
+    b1 = b2;
+    b2 = bf;
+    vb ^= 1;
+    lkb = sk.kb + (int64_t)sk.t * (kBN * KROW);
+    lkd = lds0 + b2 * KT;
+    lvb = sv.vb + sv.t * (kBN * 2);
+    lvrs = sv.vrs2;
+    lvd = lds0 + 3 * KT + (vb ^ 1) * VT;
+    ks2 = load_ks(sk);
+    sv = sk;
+    stream_next<true>(sk, a, h);
+    nv3 = tile_valid(sk);
+  }
+
+  // ---- epilogue (as the kernel above)
+  wait_vmem();
+  drain_o();
+  if (part >= 0) {
+    float *wo = a.ws + (int64_t)(blockIdx.x - a.full) * (kBM * D + kBM);
+#pragma unroll
+    for (int hf = 0; hf < 2; ++hf) {
+      const float lt = lsum[hf] + __shfl_xor(lsum[hf], 32);
+      const float inv = 1.0f / lt;
+      const int rl = w * kQW + hf * 32 + lr;
       if (q0 + hf * 32 + lr < a.lq) {
         float *op = wo + rl * D + 4 * g;
 #pragma unroll
@@ -1130,9 +1537,10 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   k.nsplit = 1;
   int rem = 0;
   if (args->split_workspace) {
-    const int cus = device_cus();
-    const int n = choose_split((int)items, cus, k.ntiles);
-    rem = n > 1 ? (int)(items % cus) : 0;
+    // workgroups resident at once: one per CU (BF16), two per CU (INT8-QK)
+    const int slots = (I8 ? 2 : 1) * device_cus();
+    const int n = choose_split((int)items, slots, k.ntiles);
+    rem = n > 1 ? (int)(items % slots) : 0;
     if (n > 1 && args->split_workspace_bytes >= (int64_t)rem * n * split_slot_bytes(args->head_dim)) {
       k.full = (int)items - rem;
       k.nsplit = n;
@@ -1143,10 +1551,14 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   }
   const unsigned grid = (unsigned)(k.full + (int64_t)rem * k.nsplit);
   hipStream_t s = (hipStream_t)stream;
-  if (args->head_dim == 128)
-    hipLaunchKernelGGL((attn_fwd_kernel<128, I8>), dim3(grid), dim3(kWaves * 64), 0, s, k);
+  if (I8 && args->head_dim == 128)
+    hipLaunchKernelGGL((attn_i8_kernel<128>), dim3(grid), dim3(kWaves * 64), 0, s, k);
+  else if (I8)
+    hipLaunchKernelGGL((attn_i8_kernel<64>), dim3(grid), dim3(kWaves * 64), 0, s, k);
+  else if (args->head_dim == 128)
+    hipLaunchKernelGGL((attn_fwd_kernel<128>), dim3(grid), dim3(kWaves * 64), 0, s, k);
   else
-    hipLaunchKernelGGL((attn_fwd_kernel<64, I8>), dim3(grid), dim3(kWaves * 64), 0, s, k);
+    hipLaunchKernelGGL((attn_fwd_kernel<64>), dim3(grid), dim3(kWaves * 64), 0, s, k);
   const char *what = I8 ? "tmhd_attn_fwd_i8qk" : "tmhd_attn_fwd_bf16";
   int st2 = check_launch(what);
   if (st2 || rem == 0) return st2;
@@ -1209,7 +1621,8 @@ extern "C" int tmhd_attn_fwd_bf16_noalloc(const tmhd_attn_args *args, void *stre
 
 extern "C" int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim) {
   if (head_dim != 64 && head_dim != 128) return 0;
-  return (int64_t)tmhd::device_cus() * tmhd::split_slot_bytes(head_dim);
+  // the INT8-QK kernel runs two workgroups per CU, so its split round can use two slots per CU
+  return 2 * (int64_t)tmhd::device_cus() * tmhd::split_slot_bytes(head_dim);
 }
 
 extern "C" int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream) {
