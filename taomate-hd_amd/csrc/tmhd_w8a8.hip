@@ -342,20 +342,26 @@ gemm_i8_kernel(const GArgs ga) {
 
 // ---------------------------------------------------------------------------
 // INT8 GEMM, one wave per SIMD: workgroup tile 256 (m) x 256 (n), 4 waves as
-// 2 (m) x 2 (n), each wave 128 x 128 (16 MFMA blocks, 256 int32 accumulators
-// per lane in AGPRs).  A 32-byte k-step reads 4 A and 4 B operands
-// (ds_read_b128) for 16 MFMAs; the next k-step's reads are issued under the
-// current one's MFMAs, one read per MFMA.
-// k moves in blocks of 128 bytes (four k-steps).  A block's operands sit in
+// 2 (m) x 2 (n), each wave 128 x 128 (64 blocks of 16 x 16, 256 int32
+// accumulators per lane in AGPRs).  A 64-byte k-step reads 8 A and 8 B
+// operands (ds_read_b128) for 64 v_mfma_i32_16x16x64_i8; the next k-step's
+// reads are issued under the current one's MFMAs, one read per 4 MFMAs.
+// The card is power-limited under this loop, and the 16 x 16 shape moves
+// half the accumulator bytes per multiply-accumulate of the 32 x 32 one: on
+// random int8 operands an MFMA-only stream settles at 4,085 TOPS against
+// 3,430 for v_mfma_i32_32x32x32_i8 (1.96 against 1.63 GHz), and this kernel
+// runs 7% faster with it than with the 32 x 32 shape at the same tiling.
+// k moves in blocks of 128 bytes (two k-steps).  A block's operands sit in
 // two ring units, one per 128-row half of the tile (rows of 128 bytes: whole
 // cache lines, so each 1 KiB global_load_lds_dwordx4 touches 8 lines and
 // every line is fetched once -- against 16 half-used lines per load with
 // 64-byte rows, which measured 9% slower on the 12,252 x 5,120 x 13,824
 // projection and the 12,252 x 5,376 x 28,672 FC1, with the load path's
 // address unit stalled by the L1 27% of the time).  Units cycle through a
-// 5-deep ring (5 x 32 KiB, all of the CU's LDS), 3 to 7 k-steps ahead of
-// their first read; a 3-deep ring of 64-byte stages (about 4 k-steps ahead)
-// was as fast as the 5-deep one, so the shorter lookahead costs nothing.
+// 5-deep ring (5 x 32 KiB, all of the CU's LDS), 96 to 224 bytes of k ahead
+// of their first read; a 3-deep ring of 64-byte stages (about 128 bytes
+// ahead) was as fast as the 5-deep one, so the shorter lookahead costs
+// nothing.
 constexpr int HBM_ = 256, HBN = 256, HKD = 128, HWAVES = 4, HRING = 5;
 constexpr int HUNIT = 2 * 128 * HKD;  // bytes of one ring unit: 128 rows of A, then of B
 
@@ -397,8 +403,8 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   // Unit u = (k block u / 2, row half u % 2): rows [128 h, 128 h + 128) of the
   // A and the B tile over 128 bytes of k, in ring slot u % HRING (16 KiB of A,
   // then 16 KiB of B, rows of 128 bytes).  Chunk c of row r sits at
-  // c ^ ((r >> 1) & 7): the 16 rows of a ds_read_b128 phase cover both row
-  // parities and 8 chunk positions, i.e. all 16 bank groups.
+  // c ^ ((r >> 1) & 7), which keeps the operand reads free of bank conflicts
+  // (their pattern is stated with the read offsets below).
   // Loads: a unit is 16 blocks of 1 KiB (8 rows x 128 bytes: whole cache
   // lines) per operand; wave w loads blocks w, w + 4, w + 8, w + 12 of each.
   // Lane: row 8 blk + lane / 8, physical chunk lane % 8, logical chunk
@@ -424,20 +430,23 @@ gemm_i8_wave128_kernel(const GArgs ga) {
     else
       hload_lds16(bbase + (int64_t)j * HKD, boff[h][i], dst + HUNIT / 2);
   };
-  // operand read offsets within a unit's operand part, k-step q (0..3) of the
-  // block: row lr (+ 32 per block), logical chunk 2 q + g
-  uint32_t rdq[4];
+  // operand read offsets within a unit's operand part, k-step q (0..1) of the
+  // block: 16x16x64 operand lane (i, g4) = lane % 16, lane / 16 holds 16 bytes
+  // of row i (+ 16 per block) at logical chunk 4 q + g4.  A 16-byte read is
+  // served for 32 consecutive lanes at a time from 128 4-byte banks: rows
+  // i = 0..15 at two chunks, whose physical chunks under the swizzle fill all
+  // 32 16-byte bank groups of the 4 row classes (row stride 128 bytes).
+  const int li = lane & 15, lg = lane >> 4;
+  uint32_t rdq[2];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) rdq[q] = (uint32_t)(lr * HKD + (((2 * q + g) ^ ((lr >> 1) & 7)) * 16));
+  for (int q = 0; q < 2; ++q) rdq[q] = (uint32_t)(li * HKD + (((4 * q + lg) ^ ((li >> 1) & 7)) * 16));
   auto rd = [&](uint32_t off) { return *(const i32x4 *)(smem + off); };
 
-  i32x16 acc[4][4];  // [n block][m block], D[n][m]
+  i32x4 acc[8][8];  // [n block][m block], D[n][m]: lane (j, g4) holds n = 16 nb + 4 g4 + (0..3), m = 16 mb + j
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+    for (int j = 0; j < 8; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
 
   // prologue: units 0..3 in flight; units 0 and 1 (k block 0) landed
 #pragma unroll
@@ -446,68 +455,65 @@ gemm_i8_wave128_kernel(const GArgs ga) {
     for (int n = 0; n < 8; ++n) load_one(u, n);
   __builtin_amdgcn_s_waitcnt(0x0f70 | 16);  // vmcnt(16): units 2, 3 may stay in flight
   __syncthreads();
-  i32x4 cur[8], nxt[8];
-  // operand r of k-step q of k block d (ring position dm = d % HRING): r < 4
-  // A block r from unit 2 d + wm, else B block r - 4 from unit 2 d + wn
+  i32x4 cur[16], nxt[16];
+  // operand r of k-step q of k block d (ring position dm = d % HRING): r < 8
+  // A block r from unit 2 d + wm, else B block r - 8 from unit 2 d + wn
   auto read_op = [&](int dm, int q, int r) -> i32x4 {
-    if (r < 4) return rd((uint32_t)(((2 * dm + wm) % HRING) * HUNIT) + rdq[q] + r * 32 * HKD);
-    return rd((uint32_t)(((2 * dm + wn) % HRING) * HUNIT + HUNIT / 2) + rdq[q] + (r - 4) * 32 * HKD);
+    if (r < 8) return rd((uint32_t)(((2 * dm + wm) % HRING) * HUNIT) + rdq[q] + r * 16 * HKD);
+    return rd((uint32_t)(((2 * dm + wn) % HRING) * HUNIT + HUNIT / 2) + rdq[q] + (r - 8) * 16 * HKD);
   };
 #pragma unroll
-  for (int r = 0; r < 8; ++r) cur[r] = read_op(0, 0, r);
+  for (int r = 0; r < 16; ++r) cur[r] = read_op(0, 0, r);
 
   // Epilogue operands: the column scales and bias of n-block i (the lane's
-  // columns n = n0 + wn 128 + 32 i + 8 u + 4 g + (0..3), u = 0..3) and the
-  // row scales of the lane's 4 m-blocks.  The staged epilogue loads n-block
-  // i + 1's while it converts n-block i; a tile that lies inside the matrix in
-  // n loads n-block 0's and the row scales during its last k block, so that
-  // their latency hides under its MFMAs.
+  // columns n = n0 + wn 128 + 16 i + 4 g4 + (0..3)) and the row scales of the
+  // lane's 8 m-blocks.  The staged epilogue loads n-block i + 1's while it
+  // converts n-block i; a tile that lies inside the matrix in n loads n-block
+  // 0's and the row scales during its last k block, so that their latency
+  // hides under its MFMAs.
   const bool early = !RAW && !SPLIT && ga.vec_ok && n0 + HBN <= ga.n;
-  float asv[4];
-  f32x4 bsc[4], bsn[4];
-  i32x2 bic[4], bin[4];
+  float asv[8];
+  f32x4 bsc, bsn;
+  i32x2 bic, bin;
   auto load_row_scales = [&]() {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) asv[j] = ga.as[min(m0 + wm * 128 + j * 32 + lr, ga.m - 1)];
+    for (int j = 0; j < 8; ++j) asv[j] = ga.as[min(m0 + wm * 128 + j * 16 + li, ga.m - 1)];
   };
   // VEC: the whole tile lies inside the matrix in n and the scales and bias
   // are aligned for vector loads (`early`)
-  auto load_cols = [&](auto vec_c, int i, f32x4 *bs, i32x2 *bi) {
+  auto load_cols = [&](auto vec_c, int i, f32x4 &bs, i32x2 &bi) {
     constexpr bool VEC = decltype(vec_c)::value;
+    const int n = n0 + wn * 128 + i * 16 + 4 * lg;
+    if (VEC || (ga.vec_ok && n + 3 < ga.n)) {
+      bs = *(const f32x4 *)(ga.bs + n);
+      bi = ga.bias ? *(const i32x2 *)(ga.bias + n) : i32x2{0, 0};
+    } else {
+      uint16_t bb[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
-      if (VEC || (ga.vec_ok && n + 3 < ga.n)) {
-        bs[u] = *(const f32x4 *)(ga.bs + n);
-        bi[u] = ga.bias ? *(const i32x2 *)(ga.bias + n) : i32x2{0, 0};
-      } else {
-        uint16_t bb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int nn = min(n + e, ga.n - 1);
-          bs[u][e] = ga.bs[nn];
-          bb[e] = ga.bias ? ga.bias[nn] : 0;
-        }
-        bi[u] = i32x2{(int)((uint32_t)bb[0] | ((uint32_t)bb[1] << 16)), (int)((uint32_t)bb[2] | ((uint32_t)bb[3] << 16))};
+      for (int e = 0; e < 4; ++e) {
+        const int nn = min(n + e, ga.n - 1);
+        bs[e] = ga.bs[nn];
+        bb[e] = ga.bias ? ga.bias[nn] : 0;
       }
+      bi = i32x2{(int)((uint32_t)bb[0] | ((uint32_t)bb[1] << 16)), (int)((uint32_t)bb[2] | ((uint32_t)bb[3] << 16))};
     }
   };
 
-  // k block d at ring position dm: k-steps 0..3.  MODE 0: unit 2 d + 4 is
-  // loaded under k-step 0 and unit 2 d + 5 under k-step 3, one load per two
-  // MFMAs; one barrier, in front of k-step 3: behind it, units 2 d + 2 and
-  // 2 d + 3 (block d + 1) have landed for k-step 3 to read ahead from, and
-  // nobody reads block d's units any more (k-step 3's operands are already in
-  // registers), so their slots take units 2 d + 5 and 2 d + 6.  The last two
-  // blocks load no units (none are left): MODE 1 (next to last) waits for all
-  // of its loads before the barrier; MODE 2 (last) reads nothing ahead, needs
-  // no barrier, and loads the first epilogue operands.
+  // k block d at ring position dm: k-steps 0 and 1 of 64 MFMAs.  MODE 0:
+  // unit 2 d + 4 is loaded under k-step 0 and unit 2 d + 5 under k-step 1, one
+  // load per 8 MFMAs; one barrier, in front of k-step 1: behind it, units
+  // 2 d + 2 and 2 d + 3 (block d + 1) have landed for k-step 1 to read ahead
+  // from, and nobody reads block d's units any more (k-step 1's operands are
+  // already in registers), so their slots take units 2 d + 5 and 2 d + 6.  The
+  // last two blocks load no units (none are left): MODE 1 (next to last) waits
+  // for all of its loads before the barrier; MODE 2 (last) reads nothing
+  // ahead, needs no barrier, and loads the first epilogue operands.
   auto block = [&](auto dm_v, auto mode_c, int d) {
     constexpr int MODE = decltype(mode_c)::value;
     const int dm = dm_v, dn = (dm + 1) % HRING;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      if (q == 3 && MODE != 2) {
+    for (int q = 0; q < 2; ++q) {
+      if (q == 1 && MODE != 2) {
         if (MODE == 0)
           __builtin_amdgcn_s_waitcnt(0x0f70 | 8);  // vmcnt(8): unit 2 d + 4 may stay in flight
         else
@@ -520,17 +526,18 @@ gemm_i8_wave128_kernel(const GArgs ga) {
           load_cols(std::true_type{}, 0, bsc, bic);
         }
 #pragma unroll
-      for (int idx = 0; idx < 16; ++idx) {
-        if (idx < 8 && !(MODE == 2 && q == 3)) nxt[idx] = q < 3 ? read_op(dm, q + 1, idx) : read_op(dn, 0, idx);
-        if (MODE == 0 && q == 0 && idx % 2 == 0) load_one(2 * d + 4, idx / 2);
-        if (MODE == 0 && q == 3 && idx % 2 == 0) load_one(2 * d + 5, idx / 2);
-        const int nb = idx >> 2, mb = idx & 3;
-        acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur[4 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
+      for (int idx = 0; idx < 64; ++idx) {
+        if (idx % 4 == 0 && !(MODE == 2 && q == 1))
+          nxt[idx / 4] = q == 0 ? read_op(dm, 1, idx / 4) : read_op(dn, 0, idx / 4);
+        if (MODE == 0 && q == 0 && idx % 8 == 0) load_one(2 * d + 4, idx / 8);
+        if (MODE == 0 && q == 1 && idx % 8 == 0) load_one(2 * d + 5, idx / 8);
+        const int nb = idx >> 3, mb = idx & 7;
+        acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[8 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (!(MODE == 2 && q == 3))
+      if (!(MODE == 2 && q == 1))
 #pragma unroll
-        for (int r = 0; r < 8; ++r) cur[r] = nxt[r];
+        for (int r = 0; r < 16; ++r) cur[r] = nxt[r];
     }
   };
   using M0 = std::integral_constant<int, 0>;
@@ -556,16 +563,10 @@ gemm_i8_wave128_kernel(const GArgs ga) {
     // k-range of a split tile: the raw 256 x 256 int32 partial, row-major
     int32_t *wp = ga.ws + ((int64_t)(L - ga.full) * ga.nsplit + part) * (HBM_ * HBN);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = wm * 128 + j * 32 + lr;
+    for (int j = 0; j < 8; ++j) {
+      const int m = wm * 128 + j * 16 + li;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int n = wn * 128 + i * 32 + 8 * u + 4 * g;
-          *(i32x4 *)(wp + m * HBN + n) =
-              i32x4{acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
-        }
+      for (int i = 0; i < 8; ++i) *(i32x4 *)(wp + m * HBN + wn * 128 + i * 16 + 4 * lg) = acc[i][j];
     }
     return;
   }
@@ -573,9 +574,13 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   if constexpr (!RAW) {
     if (ga.st_ok) {
       // bf16 tile through LDS: each wave stages its 128 x 128 outputs in rows
-      // of 256 + 16 bytes, then writes 16 bytes per lane, 256-byte row segments
-      constexpr int ROWB = 128 * 2 + 16;
+      // of 256 bytes whose 16-byte chunk c sits at c ^ stg_sw(row), then
+      // writes 16 bytes per lane, 256-byte row segments.  A staging write (8
+      // bytes per lane) covers 16 rows x 2 chunks, a read 2 rows x 16 chunks:
+      // under the swizzle both meet every bank once.
+      constexpr int ROWB = 128 * 2;
       static_assert(HWAVES * 128 * ROWB <= HRING * HUNIT, "staging fits the ring");
+      auto stg_sw = [](int row) { return 2 * ((row >> 1) & 7); };
       __syncthreads();  // every wave is done with the ring
       const uint32_t wt = (uint32_t)(w * 128 * ROWB);
       if (!early) {
@@ -589,40 +594,35 @@ gemm_i8_wave128_kernel(const GArgs ga) {
       auto stage_tile = [&](auto has_bias, auto vec_c) {
         constexpr bool HB = decltype(has_bias)::value;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i < 3) load_cols(vec_c, i + 1, bsn, bin);
-          float bf[4][4];
+        for (int i = 0; i < 8; ++i) {
+          if (i < 7) load_cols(vec_c, i + 1, bsn, bin);
+          float bf[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u)
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t bw = (uint32_t)bic[e >> 1];
+            bf[e] = HB ? bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu)) : 0.0f;
+          }
+          const int ch = 2 * i + (lg >> 1);  // 16-byte chunk of the lane's 4 columns
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            uint16_t vals[4];
+            float tv[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              const uint32_t bw = (uint32_t)bic[u][e >> 1];
-              bf[u][e] = HB ? bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu)) : 0.0f;
+              float t = (float)acc[i][j][e];
+              t = t * bsc[e];
+              t = t * asv[j];
+              if constexpr (HB) t = t + bf[e];
+              tv[e] = t;
             }
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-              uint16_t vals[4];
-              float tv[4];
-#pragma unroll
-              for (int e = 0; e < 4; ++e) {
-                float t = (float)acc[i][j][4 * u + e];
-                t = t * bsc[u][e];
-                t = t * asv[j];
-                if constexpr (HB) t = t + bf[u][e];
-                tv[e] = t;
-              }
-              bf16_quad(tv, vals);
-              *(i32x2 *)(smem + wt + (j * 32 + lr) * ROWB + (i * 32 + 8 * u + 4 * g) * 2) =
-                  i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
-                        (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
-            }
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            bsc[u] = bsn[u];
-            bic[u] = bin[u];
+            bf16_quad(tv, vals);
+            const int row = j * 16 + li;
+            *(i32x2 *)(smem + wt + row * ROWB + (ch ^ stg_sw(row)) * 16 + (lg & 1) * 8) =
+                i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                      (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
           }
+          bsc = bsn;
+          bic = bin;
         }
       };
       if (early) {
@@ -644,8 +644,9 @@ gemm_i8_wave128_kernel(const GArgs ga) {
         for (int it = 0; it < 16; ++it) {
           const int r = w * 64 + it * 4 + (lane >> 4), c = lane & 15;
           const int wr = r >> 7, rr = r & 127;
-          const i32x4 gv = *(const i32x4 *)(smem + (uint32_t)((wr * 2) * 128 * ROWB + rr * ROWB + c * 16));
-          const i32x4 uv = *(const i32x4 *)(smem + (uint32_t)((wr * 2 + 1) * 128 * ROWB + rr * ROWB + c * 16));
+          const uint32_t so = (uint32_t)(rr * ROWB + (c ^ stg_sw(rr)) * 16);
+          const i32x4 gv = *(const i32x4 *)(smem + (uint32_t)((wr * 2) * 128 * ROWB) + so);
+          const i32x4 uv = *(const i32x4 *)(smem + (uint32_t)((wr * 2 + 1) * 128 * ROWB) + so);
           i32x4 o;
 #pragma unroll
           for (int e = 0; e < 4; ++e) o[e] = (int)swiglu_pair((uint32_t)gv[e], (uint32_t)uv[e]);
@@ -657,7 +658,7 @@ gemm_i8_wave128_kernel(const GArgs ga) {
 #pragma unroll
       for (int it = 0; it < 32; ++it) {
         const int r = it * 4 + (lane >> 4), c = lane & 15;
-        const i32x4 v = *(const i32x4 *)(smem + wt + r * ROWB + c * 16);
+        const i32x4 v = *(const i32x4 *)(smem + wt + r * ROWB + (c ^ stg_sw(r)) * 16);
         const int m = m0 + wm * 128 + r, n = n0 + wn * 128 + c * 8;
         if (m < ga.m && n < ga.n) {
           uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
@@ -674,46 +675,43 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   if constexpr (GLU) return;  // the GLU launcher always takes the staged path above
   // unstaged epilogue (bf16 rows not 16-byte aligned) and the raw int32 output
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
+  for (int i = 0; i < 8; ++i) {
     if constexpr (!RAW) load_cols(std::false_type{}, i, bsc, bic);
+    const int n = n0 + wn * 128 + i * 16 + 4 * lg;
+    if (n >= ga.n) continue;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int m = m0 + wm * 128 + j * 32 + lr;
+    for (int j = 0; j < 8; ++j) {
+      const int m = m0 + wm * 128 + j * 16 + li;
       if (m >= ga.m) continue;
-      const float asm_ = RAW ? 0.0f : ga.as[m];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int n = n0 + wn * 128 + i * 32 + 8 * u + 4 * g;
-        if (n >= ga.n) continue;
-        if constexpr (RAW) {
-          int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
-          if (n + 3 < ga.n) {
-            *(i32x4 *)op = i32x4{acc[i][j][4 * u], acc[i][j][4 * u + 1], acc[i][j][4 * u + 2], acc[i][j][4 * u + 3]};
-          } else {
-            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[i][j][4 * u + e];
-          }
+      if constexpr (RAW) {
+        int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
+        if (n + 3 < ga.n) {
+          *(i32x4 *)op = acc[i][j];
         } else {
-          uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
-          uint16_t vals[4];
-          float tv[4];
+          for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[i][j][e];
+        }
+      } else {
+        const float asm_ = ga.as[m];
+        uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+        uint16_t vals[4];
+        float tv[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float t = (float)acc[i][j][4 * u + e];
-            t = t * bsc[u][e];
-            t = t * asm_;
-            if (ga.bias) {
-              const uint32_t bw = (uint32_t)bic[u][e >> 1];
-              t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
-            }
-            tv[e] = t;
+        for (int e = 0; e < 4; ++e) {
+          float t = (float)acc[i][j][e];
+          t = t * bsc[e];
+          t = t * asm_;
+          if (ga.bias) {
+            const uint32_t bw = (uint32_t)bic[e >> 1];
+            t = t + bf16_bits_to_f32((e & 1) ? (bw >> 16) : (bw & 0xffffu));
           }
-          bf16_quad(tv, vals);
-          if (n + 3 < ga.n) {
-            *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
-                                 (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
-          } else {
-            for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
-          }
+          tv[e] = t;
+        }
+        bf16_quad(tv, vals);
+        if (n + 3 < ga.n) {
+          *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                               (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+        } else {
+          for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
         }
       }
     }
