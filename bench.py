@@ -647,7 +647,7 @@ def main() -> int:
         result["components_ms"] = {k: round(v["mean_ms"], 4) for k, v in comps.items()}
         result["roofline"] = roofline(
             achieved, PEAK_BF16_TFLOPS, "mfma", "TFLOP/s", "attn_fwd_bf16_768p_pmc.txt", ATTN_SOURCE,
-            kernel="attn_fwd_kernel<128, bf16> + attn_merge_kernel<128> (split last round)",
+            kernel="attn_fwd_kernel<128> + attn_merge_kernel<128> (split last round)",
             flops_per_launch=ATTN_FLOPS, kernel_ms=round(attn_ms, 4),
             timing="HIP events around each attention call on its launch stream, timed steps only")
         _log(f"bf16: {wall_ms:.3f} ms/step (device {dev_ms:.3f}), kernel {attn_ms:.3f} ms = {achieved:.1f} TFLOPS")
@@ -676,7 +676,7 @@ def main() -> int:
             "roofline": roofline(
                 c2_flops / (c2_attn_ms * 1e-3) / 1e12, PEAK_BF16_TFLOPS, "mfma", "TFLOP/s",
                 "attn_fwd_bf16_480p_pmc.txt", ATTN_SOURCE,
-                kernel="attn_fwd_kernel<128, bf16> (+ attn_merge_kernel<128> when the last round is split)",
+                kernel="attn_fwd_kernel<128> (+ attn_merge_kernel<128> when the last round is split)",
                 flops_per_launch=c2_flops, kernel_ms=round(c2_attn_ms, 4),
                 timing="HIP events around each attention call on its launch stream, timed steps only"),
         }
@@ -715,7 +715,7 @@ def main() -> int:
             "roofline": roofline(
                 ATTN_FLOPS / (attn_ms * 1e-3) / 1e12, round(PEAK_MIXED_TFLOPS, 1), "mfma", "TFLOP/s",
                 "attn_fwd_i8qk_768p_pmc.txt", ATTN_SOURCE,
-                kernel="attn_fwd_kernel<128, i8> + attn_merge_kernel<128> (split last round)",
+                kernel="attn_i8_kernel<128>, two workgroups per CU (+ attn_merge_kernel<128> when the last round is split)",
                 peak_note="mixed peak: INT8 Q.K^T at 5,033 TOPS and BF16 P.V at 2,517 TFLOPS, half the work each",
                 flops_per_launch=ATTN_FLOPS, kernel_ms=round(attn_ms, 4)),
         }
