@@ -461,7 +461,10 @@ int tmhd_gemm_i8_i32(int32_t *out, const int8_t *a, const int8_t *b, int32_t m,
  * to the unsplit GEMM.  tmhd_gemm_split_workspace_bytes gives the bytes this
  * needs on the current device for the shape (0: no split); with a smaller or
  * null workspace the _ws calls run unsplit.  Partial tiles of calls that
- * overlap on one workspace race.
+ * overlap on one workspace race.  A last round of at most an eighth of the
+ * CUs' tiles needs no workspace in these two GEMMs: it runs as 64 x 128
+ * sub-tiles over the whole of k (bit-identical too), with or without one;
+ * the SwiGLU GEMM below splits it along k.
  */
 int64_t tmhd_gemm_split_workspace_bytes(int32_t m, int32_t n, int32_t k);
 int tmhd_gemm_w8a8_ws(void *out, const int8_t *a, const int8_t *b, const float *a_scale,

@@ -718,6 +718,161 @@ gemm_i8_wave128_kernel(const GArgs ga) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// The last, partial round of 256 x 256 tiles when it holds at most an eighth
+// of a round: each of its tiles runs as 8 sub-tiles of 64 (m) x 128 (n) over
+// the whole of k, one workgroup each, so the round fills the CUs with no
+// partial sums and no merge (the k split's int32 partials and their merge
+// cost about twice the time).  4 waves as 2 (m) x 2 (n) of 32 x 64 (8 blocks
+// of v_mfma_i32_16x16x64_i8).  k moves in blocks of 128 bytes, one ring unit
+// each (64 rows of A, then 128 rows of B, rows of 128 bytes with chunk c of
+// row r at c ^ ((r >> 1) & 7), as in the whole-tile kernel), 5 units deep;
+// block d's loads fetch unit d + 3.  The epilogue stores straight from
+// registers (the round is small) with the whole-tile kernel's arithmetic.
+constexpr int SBM = 64, SBN = 128, SRING = 5;
+constexpr int SUNIT = (SBM + SBN) * HKD;  // bytes of one ring unit
+constexpr int SLOADS = SUNIT / 1024 / 4;  // 1 KiB wave loads per wave per unit
+static_assert(SUNIT % 4096 == 0 && SRING * SUNIT <= 160 * 1024, "ring fits the LDS");
+
+template <bool RAW>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+gemm_i8_sub_kernel(const GArgs ga) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(1024))) char smem[SRING * SUNIT];
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)smem;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;  // wave tile: a rows [wm*32, +32), b rows [wn*64, +64)
+  // item L: sub-tile L % 8 of tile full + L / 8; the 8 sub-tiles of a tile are
+  // consecutive logical ids, which run on one XCD (its L2 holds their panels)
+  const int L = xcd_logical_id(blockIdx.x, gridDim.x);
+  const int sub = L & 7;
+  int tm, tn;
+  grouped_tile(ga.full + (L >> 3), ga.tm_count, ga.tn_count, tm, tn);
+  const int m0 = tm * HBM_ + (sub >> 1) * SBM, n0 = tn * HBN + (sub & 1) * SBN;
+  if (m0 >= ga.m || n0 >= ga.n) return;  // the whole workgroup: no barrier is left waiting
+  const int nd = ga.k / HKD;  // >= 1
+
+  // Loads: block b (0..23) of a unit is 8 rows x 128 bytes: b < 8 the A rows
+  // 8 b .., else the B rows 8 (b - 8) ..; wave w loads blocks w + 4 i.  Lane:
+  // row 8 blk + lane / 8, physical chunk lane % 8, logical chunk
+  // (lane % 8) ^ ((row >> 1) & 7), the same for all of the wave's blocks
+  // (their parity is w's).
+  const int lch = (lane & 7) ^ ((4 * (w & 1) + (lane >> 4)) & 7);
+  uint32_t soff[SLOADS];
+#pragma unroll
+  for (int i = 0; i < SLOADS; ++i) {
+    const int b = w + 4 * i;
+    if (b < SBM / 8)
+      soff[i] = (uint32_t)((int64_t)min(m0 + b * 8 + (lane >> 3), ga.m - 1) * ga.lda) + lch * 16;
+    else
+      soff[i] = (uint32_t)((int64_t)min(n0 + (b - SBM / 8) * 8 + (lane >> 3), ga.n - 1) * ga.ldb) + lch * 16;
+  }
+  // unit u (k block min(u, nd - 1): units past the last block repeat it, into
+  // a slot nobody reads) into ring slot u % SRING
+  auto load_unit = [&](int u) {
+    const int64_t k0 = (int64_t)min(u, nd - 1) * HKD;
+    const uint32_t dst = lds0 + (uint32_t)((u % SRING) * SUNIT);
+#pragma unroll
+    for (int i = 0; i < SLOADS; ++i) {
+      const int b = w + 4 * i;
+      hload_lds16((b < SBM / 8 ? ga.a : ga.b) + k0, soff[i], dst + b * 1024);
+    }
+  };
+  // operand reads: 16x16x64 lane (i, g4) holds 16 bytes of row i at logical
+  // chunk 4 q + g4 (k-step q of the block)
+  const int li = lane & 15, lg = lane >> 4;
+  uint32_t rdq[2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) rdq[q] = (uint32_t)(li * HKD + (((4 * q + lg) ^ ((li >> 1) & 7)) * 16));
+  // operand r of k-step q of unit u: r < 2 A block r, else B block r - 2
+  auto read_op = [&](int u, int q, int r) -> i32x4 {
+    const uint32_t base = (uint32_t)((u % SRING) * SUNIT) + rdq[q];
+    if (r < 2) return *(const i32x4 *)(smem + base + (wm * 32 + 16 * r) * HKD);
+    return *(const i32x4 *)(smem + base + SBM * HKD + (wn * 64 + 16 * (r - 2)) * HKD);
+  };
+
+  i32x4 acc[4][2];  // [n block][m block], D[n][m]: lane (j, g4) holds n = 16 nb + 4 g4 + (0..3), m = 16 mb + j
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+  // prologue: units 0..2 in flight, unit 0 landed
+  load_unit(0);
+  load_unit(1);
+  load_unit(2);
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * SLOADS));  // units 1, 2 may stay in flight
+  __syncthreads();
+  i32x4 cur[6], nxt[6];
+#pragma unroll
+  for (int r = 0; r < 6; ++r) cur[r] = read_op(0, 0, r);
+  // block d: k-step 0 loads unit d + 3 into the slot of unit d - 2 (every
+  // wave is past block d - 2: the barrier of block d - 1) and reads k-step 1's
+  // operands; k-step 1 waits for unit d + 1 (units d + 2 and d + 3 may stay in
+  // flight), passes the barrier and reads block d + 1's first operands.
+  for (int d = 0; d < nd; ++d) {
+    load_unit(d + 3);
+#pragma unroll
+    for (int r = 0; r < 6; ++r) nxt[r] = read_op(d, 1, r);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[2 + nb], cur[mb], acc[nb][mb], 0, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0f70 | (2 * SLOADS));
+    __syncthreads();
+    if (d + 1 < nd)
+#pragma unroll
+      for (int r = 0; r < 6; ++r) cur[r] = read_op(d + 1, 0, r);
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) acc[nb][mb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(nxt[2 + nb], nxt[mb], acc[nb][mb], 0, 0, 0);
+  }
+  // every wave drains its loads before the workgroup ends
+  __builtin_amdgcn_s_waitcnt(0x0f70);
+
+  // epilogue straight from registers: 4 consecutive n of one m per lane
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+    const int n = n0 + wn * 64 + nb * 16 + 4 * lg;
+    if (n >= ga.n) continue;
+    float bsv[4];
+    uint16_t bbv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int nn = min(n + e, ga.n - 1);
+      bsv[e] = RAW ? 0.0f : ga.bs[nn];
+      bbv[e] = (!RAW && ga.bias) ? ga.bias[nn] : 0;
+    }
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int m = m0 + wm * 32 + mb * 16 + li;
+      if (m >= ga.m) continue;
+      if constexpr (RAW) {
+        int32_t *op = (int32_t *)ga.out + (int64_t)m * ga.ldo + n;
+        if (n + 3 < ga.n)
+          *(i32x4 *)op = acc[nb][mb];
+        else
+          for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = acc[nb][mb][e];
+      } else {
+        const float asm_ = ga.as[m];
+        uint16_t vals[4];
+        float tv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tv[e] = dequant_f32(acc[nb][mb][e], bsv[e], asm_, ga.bias != nullptr, bbv[e]);
+        bf16_quad(tv, vals);
+        uint16_t *op = (uint16_t *)ga.out + (int64_t)m * ga.ldo + n;
+        if (n + 3 < ga.n && ga.st_ok)
+          *(i32x2 *)op = i32x2{(int)((uint32_t)vals[0] | ((uint32_t)vals[1] << 16)),
+                               (int)((uint32_t)vals[2] | ((uint32_t)vals[3] << 16))};
+        else
+          for (int e = 0; e < 4 && n + e < ga.n; ++e) op[e] = vals[e];
+      }
+    }
+  }
+}
+
 // Merge of the K-split GLU tiles: gate columns c .. c + 3 and up columns
 // 128 + c .. of one row, each the sum of its partials, dequantised and
 // rounded as the GEMM's epilogue does, then SwiGLU.  Block: 8 rows of one
@@ -831,6 +986,19 @@ int launch_gemm(void *out, const int8_t *a, const int8_t *b, const float *as, co
   const bool wide = (int64_t)(m - 1) * lda + k < ((int64_t)1 << 32) &&
                     (int64_t)(n - 1) * ldb + k < ((int64_t)1 << 32);
   if (wide && k % HKD == 0) {
+    // a last round of at most an eighth of the CUs' tiles runs as 64 x 128
+    // sub-tiles over the whole of k (no workspace needed); a larger partial
+    // round, up to half the CUs, is split along k into the workspace
+    const int cus = device_cus();
+    const int64_t last = cus > 0 ? tiles % cus : 0;
+    if (last > 0 && 8 * last <= cus) {
+      ga.full = (int32_t)(tiles - last);
+      hipStream_t s = (hipStream_t)stream;
+      if (ga.full > 0)
+        hipLaunchKernelGGL((gemm_i8_wave128_kernel<RAW, false>), dim3((unsigned)ga.full), dim3(HWAVES * 64), 0, s, ga);
+      hipLaunchKernelGGL((gemm_i8_sub_kernel<RAW>), dim3((unsigned)(last * 8)), dim3(256), 0, s, ga);
+      return check_launch(what);
+    }
     int tail = 0, parts = 1;
     gemm_split_plan(m, n, k, tail, parts);
     if (parts > 1 && ws && ((uintptr_t)ws % 16) == 0 && ws_bytes >= gemm_split_bytes(tail, parts)) {

@@ -356,12 +356,17 @@ def test_gemm_accumulators_and_epilogue_bit_exact(torch_mod, dev, m, n, k):
 
 
 def test_gemm_split_round_equals_unsplit(torch_mod, dev):
-    # 15 x 18 = 270 tiles: on 256 CUs one whole round plus a 14-tile round that
-    # is split along k; the split + merge must equal the unsplit GEMM bit for bit
+    # 8 x 37 = 296 tiles: on 256 CUs one whole round plus a 40-tile round (more
+    # than an eighth of the CUs, at most half) that is split along k; the
+    # split + merge must equal the unsplit GEMM bit for bit
     torch = torch_mod
     from taomate_hd_amd import _native, quant
 
-    m, n, k = 15 * 256 - 100, 18 * 256 - 30, 1024
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    m, n, k = 8 * 256 - 100, 37 * 256 - 30, 1024
+    last = (8 * 37) % cus
+    if not (cus < 8 * last and 2 * last <= cus):
+        pytest.skip(f"296 tiles leave a last round of {last} on {cus} CUs: not the k-split case")
     rng = np.random.default_rng(5)
     ad = torch.from_numpy(rng.integers(-128, 128, size=(m, k), dtype=np.int8)).to(dev)
     wd = torch.from_numpy(rng.integers(-127, 128, size=(n, k), dtype=np.int8)).to(dev)
@@ -383,6 +388,37 @@ def test_gemm_split_round_equals_unsplit(torch_mod, dev):
     out = quant.cutlass_scaled_mm(ad, wd.t(), sa.view(m, 1), sb.view(1, n), torch.bfloat16, bias)
     torch.cuda.synchronize()
     assert torch.equal(ref.view(torch.int16), out.view(torch.int16))
+
+
+def test_gemm_sub_tile_last_round(torch_mod, dev):
+    # 15 x 18 = 270 tiles: on 256 CUs one whole round plus a 14-tile round (at
+    # most an eighth of the CUs), which runs as 64 x 128 sub-tiles over the
+    # whole of k; int32 accumulators against an exact float64 product, and the
+    # bf16 epilogue against the oracle, bit for bit (k = 384: a 3-block ring)
+    torch = torch_mod
+    from taomate_hd_amd import quant
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    m, n, k = 15 * 256 - 100, 18 * 256 - 30, 384
+    last = (15 * 18) % cus
+    if not (0 < 8 * last <= cus):
+        pytest.skip(f"270 tiles leave a last round of {last} on {cus} CUs: not the sub-tile case")
+    rng = np.random.default_rng(9)
+    a = rng.integers(-128, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    ad, wd = torch.from_numpy(a).to(dev), torch.from_numpy(w).to(dev)
+    acc = quant.int8_mm_i32(ad, wd.t())
+    sa = rng.random(m, dtype=np.float32) * 0.05 + 1e-3
+    sb = rng.random(n, dtype=np.float32) * 0.01 + 1e-4
+    bias = randn_bf16((n,), 62, std=0.02)
+    out = quant.cutlass_scaled_mm(ad, wd.t(), torch.from_numpy(sa).to(dev).view(m, 1),
+                                  torch.from_numpy(sb).to(dev).view(1, n), torch.bfloat16, to_dev(bias, dev))
+    torch.cuda.synchronize()
+    want = (a.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)  # exact: |sum| < 2^53
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), want)
+    got = bf16.from_torch(out)
+    exp = oq.scaled_mm_epilogue(want.astype(np.int32), sa, sb, bias)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
 
 
 @pytest.mark.parametrize("backend", ["bf16", "i8qk"])

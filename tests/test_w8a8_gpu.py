@@ -74,9 +74,10 @@ def test_w8a8_projection_full_size_sampled_rows(torch_mod, dev):
     """The 768p projection at full size (12,252 x 5,120 -> 13,824, bf16 bias)
     on the projection workload's distribution (X ~ N(0, 1) with 1% of the
     channels, 51, scaled by 20; W ~ N(0, 0.02)): the whole GEMM runs (whole
-    tiles, the k-split last round and its merge); 24 rows, spread over every
-    row tile, are checked bit for bit against the oracle (token quantization
-    is per row, so sampled rows stand alone)."""
+    tiles, and the 32-tile last round as 64 x 128 sub-tiles); 24 rows, spread
+    over the row tiles (row 11,276 lies in the last round's tiles), are
+    checked bit for bit against the oracle (token quantization is per row, so
+    sampled rows stand alone)."""
     torch = torch_mod
     from taomate_hd_amd import cutlass_w8a8_linear, quantize_cutlass_w8a8_weight
 
