@@ -127,8 +127,10 @@ int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream);
 
 /*
  * Bytes of split_workspace that let every attention call with this head_dim
- * on the current device split its last round, on either backend (two
- * [256][head_dim + 1] fp32 slots per CU; 0 for an unsupported head_dim).  Has no counterpart in the reference: the reference's SDPA /
+ * on the current device split its last round, on either backend (six
+ * [256][head_dim + 1] fp32 slots per CU: the INT8-QK split round can run up
+ * to three sub-rounds of two workgroups per CU; 0 for an unsupported
+ * head_dim).  Has no counterpart in the reference: the reference's SDPA /
  * SageAttention calls manage their own scratch.
  */
 int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim);

@@ -1450,6 +1450,32 @@ int choose_split(int items, int cus, int ntiles) {
   return n > 1 ? n : 1;
 }
 
+// The INT8-QK kernel's last round, over `slots` resident workgroups (two per
+// CU): the rem items it holds run as n key ranges each, n (at most 8, each
+// range at least 4 key tiles, rem * n within the workspace's max_parts)
+// chosen to make the round shortest, ceil(rem * n / slots) sub-rounds of 1 / n
+// of an item (the earliest n on ties).  A round that fills three quarters of
+// the slots, as at 768p (1,920 items on 512 slots: 384), runs as 4 ranges in 3
+// full sub-rounds, 0.75 of an item instead of 1; a round of at most half the
+// slots gets the choose_split ranges.
+int choose_split_i8(int items, int slots, int ntiles, int64_t max_parts) {
+  if (slots <= 0) return 1;
+  const int rem = items % slots;
+  if (rem == 0) return 1;
+  int best = 1;
+  int64_t best_rounds = 1, best_n = 1;  // the round lasts best_rounds / best_n items
+  for (int n = 2; n <= 8 && n <= ntiles / 4; ++n) {
+    if ((int64_t)rem * n > max_parts) break;
+    const int64_t rounds = ((int64_t)rem * n + slots - 1) / slots;
+    if (rounds * best_n < best_rounds * n) {
+      best = n;
+      best_rounds = rounds;
+      best_n = n;
+    }
+  }
+  return best;
+}
+
 int build_kargs(const tmhd_attn_args *args, const tmhd_qk_quant *qq, bool i8, KArgs *k) {
   if (!args) return set_error(TMHD_ERR_INVALID, "attention: null args");
   const int D = args->head_dim;
@@ -1539,7 +1565,9 @@ int launch_attn(const tmhd_attn_args *args, const tmhd_qk_quant *qq, void *strea
   if (args->split_workspace) {
     // workgroups resident at once: one per CU (BF16), two per CU (INT8-QK)
     const int slots = (I8 ? 2 : 1) * device_cus();
-    const int n = choose_split((int)items, slots, k.ntiles);
+    const int n = I8 ? choose_split_i8((int)items, slots, k.ntiles,
+                                       args->split_workspace_bytes / split_slot_bytes(args->head_dim))
+                     : choose_split((int)items, slots, k.ntiles);
     rem = n > 1 ? (int)(items % slots) : 0;
     if (n > 1 && args->split_workspace_bytes >= (int64_t)rem * n * split_slot_bytes(args->head_dim)) {
       k.full = (int)items - rem;
@@ -1621,8 +1649,9 @@ extern "C" int tmhd_attn_fwd_bf16_noalloc(const tmhd_attn_args *args, void *stre
 
 extern "C" int64_t tmhd_attn_split_workspace_bytes(int32_t head_dim) {
   if (head_dim != 64 && head_dim != 128) return 0;
-  // the INT8-QK kernel runs two workgroups per CU, so its split round can use two slots per CU
-  return 2 * (int64_t)tmhd::device_cus() * tmhd::split_slot_bytes(head_dim);
+  // the INT8-QK kernel runs two workgroups per CU, and its split round can
+  // take up to three sub-rounds of them
+  return 3 * 2 * (int64_t)tmhd::device_cus() * tmhd::split_slot_bytes(head_dim);
 }
 
 extern "C" int tmhd_attn_fwd_bf16(const tmhd_attn_args *args, void *stream) {
