@@ -50,7 +50,7 @@ typedef struct tmhd_kv_segment {
   const void *vt;         /* bf16 slot values, transposed and interleaved */
   int64_t k_head_stride;  /* elements between heads of k (>= cap*D) */
   int64_t vt_head_stride; /* elements between heads of vt (>= D*cap) */
-  int32_t vt_row_stride;  /* elements between d rows of vt (= cap) */
+  int32_t vt_row_stride;  /* elements between d rows of vt (= cap; below 2^23) */
   int32_t tokens;         /* valid tokens, 0 < tokens <= cap */
 } tmhd_kv_segment;
 

@@ -11,9 +11,9 @@
 //   workgroup = 4 waves = 256 query rows of one head, one workgroup per CU and
 //   one wave per SIMD.  Each wave owns 64 query rows (two 32-row halves) and
 //   keeps their query operands and fp32 output accumulators in AGPRs at fixed
-//   registers, the score chain starts (BF16: -m per half; INT8: the magic
-//   constant) at fixed VGPRs v[224:255], and the scores, probabilities and
-//   online-softmax state in the other VGPRs.  Fixed registers keep the
+//   registers, the score chain starts (BF16: -m per half) at fixed VGPRs
+//   v[224:255], and the scores, probabilities and online-softmax state in
+//   the other VGPRs.  Fixed registers keep the
 //   compiler from moving these long-lived values around the loop.
 //   Keys and values stream through LDS in 64-token tiles, triple-buffered
 //   (tile t in buffer t % 3) and loaded with global_load_lds_dwordx4 (no
@@ -31,9 +31,10 @@
 //   BF16: the query is pre-scaled by scale*log2(e) (rounded to bf16 once) and
 //   the score accumulator starts at -m (m = the column's running reference),
 //   so the MFMA output is already the exponent: p = exp2(acc).
-//   INT8: the int32 accumulator starts at 0x4B400000, so its bits read as the
-//   float 1.5*2^23 + q.k exactly (|q.k| <= 127^2 * 128 < 2^22), and one FMA per
-//   score applies the per-block dequantisation scale and -m.
+//   INT8: the int32 accumulator starts at the MFMA's inline constant 1/(2 pi),
+//   bits 0x3E22F983, so its bits read as the float 0x1.45f306p-3 + q.k * 2^-26
+//   exactly (the mantissa 0x22F983 = 2,292,099 exceeds |q.k| <= 128^3), and
+//   one FMA per score applies the per-block dequantisation scale and -m.
 //   The reference m only moves (and O, l are rescaled) when a tile's score
 //   exceeds it by 2^8 (lazy rescale); P values stay <= 2^8.
 //
@@ -73,8 +74,11 @@ constexpr int kBM = kWaves * kQW;  // query rows per workgroup
 constexpr int kBN = 64;            // keys per tile
 constexpr float kLazyRescale = 8.0f;
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kI8Magic = 0x4B400000;  // bits of 1.5 * 2^23
-constexpr float kI8MagicF = 12582912.0f;
+// INT8 score chain start: the inline constant 1/(2 pi) of the integer MFMA
+// adds its bits, 0x3E22F983, to q.k; read as a float the sum is
+// kI8MagicF + q.k * 2^-26 while |q.k| < 0x22F983
+constexpr float kI8MagicF = 0x1.45f306p-3f;
+constexpr float kI8Slope = 0x1p-26f;
 
 struct Seg {
   const uint16_t *k;
@@ -904,9 +908,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 // registers.  INT8 query operands take 32 per lane (BF16: 64), and with:
 //   * all operands and accumulators in VGPRs (a kernel that touches AGPRs
 //     gets them split 128 / 128, and the output accumulators alone fill 128);
-//   * the score chains starting at the MFMA's inline constant 0, each score
-//     converted (v_cvt_f32_i32) and dequantised with the reference folded in
-//     (one FMA);
+//   * the score chains starting at the MFMA's inline constant 1/(2 pi), so
+//     each int32 score reads as a float and is dequantised with the reference
+//     folded in by one FMA (no conversion, no chain-start registers);
 //   * one score buffer: the next sub-tile's scores are converted,
 //     exponentiated and packed to bf16 under the current sub-tile's P.V
 //     MFMAs, so only the packed probabilities (16 registers) are double-buffered;
@@ -970,13 +974,13 @@ constexpr bool plan8_valid(const SlotPlan8 &s, int nqk, int npv, int db, int nld
 }
 
 // S^T (+)= K Q^T for one 32-byte k-step, all in VGPRs; `first` starts the
-// chain at 0.  Volatile, like every MFMA of this kernel: the hazard waits in
+// chain at the inline constant 1/(2 pi) (bits 0x3E22F983).  Volatile, like every MFMA of this kernel: the hazard waits in
 // front of VALU reads of MFMA results (mfma_drain, the score guard) are
 // volatile asm too, and only volatile asm keeps its order relative to them (a
 // plain asm MFMA may be sunk below a drain that does not name its registers).
-__device__ __forceinline__ void qk_i8z(bool first, i32x16 &d, i32x4 k, const i32x4 &q, const i32x16 &c) {
+__device__ __forceinline__ void qk_i8z(bool first, i32x16 &d, i32x4 k, const i32x4 &q) {
   if (first)
-    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(d) : "v"(k), "v"(q), "v"(c));
+    asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494309189532" : "=&v"(d) : "v"(k), "v"(q));
   else
     asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(d) : "v"(k), "v"(q));
 }
@@ -1039,7 +1043,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     for (int st = 0; st < QST; ++st) qv[hf][st] = ql < a.lq ? *(const i32x4 *)(p + st * 32) : i32x4{0, 0, 0, 0};
   }
   // softmax scale * log2(e) * query block scale (the wave's 64 rows lie in one 128-row block)
-  const float cq = a.c * a.qs[(int64_t)h * a.qshs + q0 / TMHD_QUANT_BLOCK];
+  const float cq = a.c * a.qs[(int64_t)h * a.qshs + q0 / TMHD_QUANT_BLOCK] * (1.0f / kI8Slope);
 
   const uint32_t kro = lr * KRS + g * 16;
   const uint32_t vro = 3 * KT + lr * VRS + g * 16;
@@ -1062,7 +1066,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 #pragma unroll
     for (int i = 0; i < VWL; ++i) {
       const int c = vblk(i) * 64 + lane, row = c / 9, chunk = min(c - row * 9, 7);
-      tab[KWL + i] = (uint32_t)row | ((uint32_t)chunk << 20);
+      tab[KWL + i] = (uint32_t)row | ((uint32_t)chunk << 28);  // chunk * 16 in the top byte
     }
     *(i32x4 *)(smem + TAB + tid * 32) = i32x4{(int)tab[0], (int)tab[1], (int)tab[2], (int)tab[3]};
     *(i32x4 *)(smem + TAB + tid * 32 + 16) = i32x4{(int)tab[4], (int)tab[5], (int)tab[6], (int)tab[7]};
@@ -1075,7 +1079,9 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       t[4 + e] = (uint32_t)hi[e];
     }
   };
-  auto voff = [&](uint32_t x, uint32_t vrs2) { return (x & 0xfffffu) * vrs2 + ((x >> 20) << 4); };
+  // row * vrs2 + chunk * 16 in one v_mad_u32_u24 (row < 128 and vrs2 < 2^24,
+  // which the launch checks; the multiply reads the low 24 bits of x)
+  auto voff = [&](uint32_t x, uint32_t vrs2) { return __umul24(x, vrs2) + (x >> 24); };
   // the tile loads go into the last NLD regions (at least the last 8); their
   // offsets are read from the table TABLEAD regions before the window
   constexpr int LWLO = 2 * NS - (NLD > 8 ? NLD : 8);
@@ -1119,9 +1125,6 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   float lsum[2] = {0.0f, 0.0f};
   float mref[2] = {0.0f, 0.0f};  // running reference of each query column (log2 units)
   i32x16 sn[2];                   // scores of the next sub-tile
-  i32x16 magic;                   // score chain start: its bits read as the float 1.5 * 2^23 + q.k
-#pragma unroll
-  for (int r = 0; r < 16; ++r) magic[r] = kI8Magic;
   // scores live as the bits of floats in i32x16 (the MFMA writes int32
   // accumulators, converted in place)
   auto f = [](int bits) { return __int_as_float(bits); };
@@ -1153,7 +1156,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     for (int st = 0; st < QST; ++st) {
       const i32x4 kv = lds_read(kb + st * 32);
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) qk_i8z(st == 0, sn[hf], kv, qv[hf][st], magic);
+      for (int hf = 0; hf < 2; ++hf) qk_i8z(st == 0, sn[hf], kv, qv[hf][st]);
     }
     drain_scores();  // the score results, and every P.V accumulation in flight
     const int t = nvalid - 4 * g;  // element r of a lane holds key 8 (r / 4) + 4 g + r % 4
@@ -1305,7 +1308,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
         }
       __builtin_amdgcn_sched_barrier(0);
       if (i < NQK) {
-        qk_i8z(i == 0, sn[hr], ops[i], qv[hr][i], magic);
+        qk_i8z(i == 0, sn[hr], ops[i], qv[hr][i]);
       } else {
         const int p = i - NQK, st = p / DB, db = p % DB;
         pv_v(o[hr][db], ops[i], pk[hr][st]);
@@ -1523,7 +1526,8 @@ int build_kargs(const tmhd_attn_args *args, const tmhd_qk_quant *qq, bool i8, KA
     if (sg.tokens <= 0) return set_error(TMHD_ERR_INVALID, "attention: segment %d has %d tokens", i, sg.tokens);
     if (!sg.k || !sg.vt || !aligned(sg.k, 16) || !aligned(sg.vt, 16))
       return set_error(TMHD_ERR_INVALID, "attention: segment %d pointers must be 16-byte aligned", i);
-    if (sg.vt_row_stride % kBN || sg.vt_row_stride < cap || sg.vt_head_stride < (int64_t)D * sg.vt_row_stride ||
+    if (sg.vt_row_stride % kBN || sg.vt_row_stride < cap || sg.vt_row_stride >= (1 << 23) ||
+        sg.vt_head_stride < (int64_t)D * sg.vt_row_stride ||
         sg.k_head_stride < cap * D || sg.vt_head_stride % 8 || sg.k_head_stride % 8)
       return set_error(TMHD_ERR_INVALID,
                        "attention: segment %d is not a slot (tokens %d, vt_row_stride %d, strides %lld/%lld)", i,

@@ -22,6 +22,9 @@ from typing import Any
 from . import _native
 
 KV_TILE = _native.KV_TILE
+# the attention kernels address a V^T row as row * 2 * capacity in 24-bit
+# multiplies: a slot holds fewer than 2^23 tokens
+MAX_SLOT_CAPACITY = (1 << 23) - KV_TILE
 
 
 def round_up(value: int, multiple: int) -> int:
@@ -78,6 +81,8 @@ class KVSlot:
         self.heads = int(heads)
         self.head_dim = int(head_dim)
         self.capacity = max(KV_TILE, round_up(capacity, KV_TILE))
+        if self.capacity > MAX_SLOT_CAPACITY:
+            raise ValueError(f"slot capacity {self.capacity} above the {MAX_SLOT_CAPACITY} tokens a slot can hold")
         self.device = torch.device(device)
         self.k = torch.empty((self.heads, self.capacity, self.head_dim), dtype=torch.bfloat16, device=self.device)
         self.vt = torch.empty((self.heads, self.head_dim, self.capacity), dtype=torch.bfloat16, device=self.device)

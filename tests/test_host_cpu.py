@@ -76,6 +76,19 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
                                                    None, 0, None), "swiglu gemm")
     with pytest.raises(ValueError, match="cols"):
         _native.check(lib.tmhd_token_quant_i8(None, None, None, 4, 12, 12, None), "quant")
+    # a V^T row stride of 2^23 tokens or more is refused (the kernels form row
+    # offsets with 24-bit multiplies); lq = 0 launches nothing when it is accepted
+    for stride, ok in (((1 << 23) - 64, True), (1 << 23, False)):
+        a = _native.AttnArgs()
+        a.q = a.o = a.seg[0].k = a.seg[0].vt = 1 << 20
+        a.heads, a.head_dim, a.scale, a.n_segments, a.lq = 1, 128, 0.125, 1, 0
+        a.seg[0].tokens, a.seg[0].vt_row_stride = 64, stride
+        a.seg[0].k_head_stride = a.seg[0].vt_head_stride = 128 * stride
+        if ok:
+            _native.check(lib.tmhd_attn_fwd_bf16(a, None), "attn")
+        else:
+            with pytest.raises(ValueError, match="not a slot"):
+                _native.check(lib.tmhd_attn_fwd_bf16(a, None), "attn")
 
 
 def test_vt_position_is_the_mfma_lane_order():
