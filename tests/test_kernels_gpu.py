@@ -204,6 +204,49 @@ def test_i8qk_attention(torch_mod, dev, heads, dim, lq, splits):
     assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
+def test_i8qk_largest_scores(torch_mod, dev, dim):
+    """Every quantized operand at +-127, so every INT8 score is +-127^2 * D
+    (2,064,512 at D 128), the largest |q.k| the path produces: each query row
+    is +-p and the keys alternate +p / -p (p a fixed +-1 pattern per head), so
+    the key mean is exactly 0.  The kernel's score chain start holds these
+    exactly; a query row of sign s attends to the keys of sign s, a uniform
+    average of their values."""
+    torch = torch_mod
+    from taomate_hd_amd import segment_attention
+
+    heads, lq, splits = 2, 256, [300, 212]
+    n = sum(splits)
+    rng = np.random.default_rng(90 + dim)
+    pat = rng.choice([-1.0, 1.0], size=(1, heads, dim)).astype(np.float32)
+    qsign = rng.choice([-1.0, 1.0], size=(lq, 1, 1)).astype(np.float32)
+    q = qsign * pat
+    k = np.where(np.arange(n) % 2 == 0, 1.0, -1.0).astype(np.float32)[:, None, None] * pat
+    v = randn_bf16((n, heads, dim), 92)
+    views = _slots(torch, dev, k, v, splits)
+    out, qv = segment_attention(
+        torch, to_dev(q, dev), views, scale=dim ** -0.5, backend="i8qk", return_quant=True
+    )
+    torch.cuda.synchronize()
+    assert np.all(np.abs(qv["q_i8"].cpu().numpy()[:, :lq].astype(np.int32)) == 127)
+    for i, s in enumerate(splits):
+        assert np.all(np.abs(qv["k_i8"][i].cpu().numpy()[:, :s].astype(np.int32)) == 127)
+    got = bf16.from_torch(out)
+    assert np.all(np.isfinite(got))
+    ksegs = np.split(k, np.cumsum(splits)[:-1])
+    vsegs = np.split(v, np.cumsum(splits)[:-1])
+    want_q, _ = oatt.i8qk_attention(q, ksegs, vsegs, dim ** -0.5)
+    mx, mean = err_stats(got, want_q)
+    assert mx <= BF16_MAX_ABS and mean <= BF16_MEAN_ABS, (mx, mean)
+    # the keys of the other sign carry exp2(-2 * 127^2 * D * scale^2 * log2 e) of the weight: none at bf16
+    even = v[0::2].astype(np.float64).mean(axis=0)
+    odd = v[1::2].astype(np.float64).mean(axis=0)
+    exact = np.where(qsign > 0, even[None], odd[None])
+    assert oatt.cosine(got, exact) >= 0.9999
+    mx, _ = err_stats(got, exact)
+    assert mx <= BF16_MAX_ABS, mx
+
+
 def test_gemm_beyond_32bit_row_offsets(torch_mod, dev):
     # a [m, k] activation of 4.3 GB: rows 524,288 and later start past 2^32 bytes,
     # so the GEMM takes the kernel with 64-bit row addressing; sampled rows on
