@@ -1050,8 +1050,8 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
 
   // per-lane source offsets of the tile loads, kept in LDS (the registers are
   // the loop's scarcest resource) and read at the start of each loading
-  // sub-tile: keys tile-invariant; values (row, chunk) packed, scaled by the
-  // segment's V^T row stride at the load
+  // sub-tile: keys tile-invariant; values for the V^T row stride of the
+  // segment the loop's value loads are in, rewritten when that changes
   auto kblk = [&](int i) { return min(w + i * kWaves, NKL - 1); };
   auto vblk = [&](int i) { return min(w + i * kWaves, NVL - 1); };
   constexpr int NLD = KWL + VWL;
@@ -1064,10 +1064,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       tab[i] = row * KROW + chunk * 16;
     }
 #pragma unroll
-    for (int i = 0; i < VWL; ++i) {
-      const int c = vblk(i) * 64 + lane, row = c / 9, chunk = min(c - row * 9, 7);
-      tab[KWL + i] = (uint32_t)row | ((uint32_t)chunk << 28);  // chunk * 16 in the top byte
-    }
+    for (int i = 0; i < VWL; ++i) tab[KWL + i] = 0;  // set by write_vtab once the streams are known
     *(i32x4 *)(smem + TAB + tid * 32) = i32x4{(int)tab[0], (int)tab[1], (int)tab[2], (int)tab[3]};
     *(i32x4 *)(smem + TAB + tid * 32 + 16) = i32x4{(int)tab[4], (int)tab[5], (int)tab[6], (int)tab[7]};
   }
@@ -1079,9 +1076,18 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       t[4 + e] = (uint32_t)hi[e];
     }
   };
-  // row * vrs2 + chunk * 16 in one v_mad_u32_u24 (row < 128 and vrs2 < 2^24,
-  // which the launch checks; the multiply reads the low 24 bits of x)
-  auto voff = [&](uint32_t x, uint32_t vrs2) { return __umul24(x, vrs2) + (x >> 24); };
+  // source offset of value load i for a V^T row stride of vrs2 bytes (row <
+  // 128 and vrs2 < 2^24, which the launch checks, so it fits 32 bits)
+  auto voff_of = [&](int i, uint32_t vrs2) {
+    const int c = vblk(i) * 64 + lane, row = c / 9, chunk = min(c - row * 9, 7);
+    return (uint32_t)row * vrs2 + (uint32_t)chunk * 16u;
+  };
+  // the lane's value offsets in the table, for row stride vrs2 (each lane
+  // reads only its own words, so no barrier is needed)
+  auto write_vtab = [&](uint32_t vrs2) {
+#pragma unroll
+    for (int i = 0; i < VWL; ++i) *(uint32_t *)(smem + TAB + tid * 32 + (KWL + i) * 4) = voff_of(i, vrs2);
+  };
   // the tile loads go into the last NLD regions (at least the last 8); their
   // offsets are read from the table TABLEAD regions before the window
   constexpr int LWLO = 2 * NS - (NLD > 8 ? NLD : 8);
@@ -1092,21 +1098,21 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   static_assert(plan8_valid(PL, NQK, NPV, DB, NLD, LWLO) && plan8_valid(PN, NQK, NPV, DB, 0, LWLO),
                 "slot plan orderings");
   auto load_one = [&](int n, const uint32_t (&t)[8], const char *kbase, uint32_t kdst, const char *vbase,
-                      uint32_t vdst, uint32_t vrs2) {
+                      uint32_t vdst) {
     if (n < KWL)
       load_lds16(kbase, t[n], kdst + kblk(n) * 1024);
     else
-      load_lds16(vbase, voff(t[n], vrs2), vdst + vblk(n - KWL) * 1024);
+      load_lds16(vbase, t[n], vdst + vblk(n - KWL) * 1024);
   };
   auto load_k = [&](const uint32_t (&t)[8], const Stream &S, int buf) {
     const char *base = S.kb + (int64_t)S.t * (kBN * KROW);
 #pragma unroll
     for (int i = 0; i < KWL; ++i) load_lds16(base, t[i], lds0 + buf * KT + kblk(i) * 1024);
   };
-  auto load_v = [&](const uint32_t (&t)[8], const Stream &S, int buf) {
+  auto load_v = [&](const Stream &S, int buf) {
     const char *base = S.vb + S.t * (kBN * 2);
 #pragma unroll
-    for (int i = 0; i < VWL; ++i) load_lds16(base, voff(t[KWL + i], S.vrs2), lds0 + 3 * KT + buf * VT + vblk(i) * 1024);
+    for (int i = 0; i < VWL; ++i) load_lds16(base, voff_of(i, S.vrs2), lds0 + 3 * KT + buf * VT + vblk(i) * 1024);
   };
   auto load_ks = [&](const Stream &S) {
     int idx = S.t >> 1;  // 128-token quant blocks hold two tiles
@@ -1213,13 +1219,14 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   stream_next<true>(t2, a, h);
   t3 = t2;
   stream_next<true>(t3, a, h);
+  write_vtab(t1.vrs2);  // the loop's first value loads are of tile 1
   __syncthreads();  // the offset table
   {
     uint32_t t[8];
     read_tab(t);
     load_k(t, t0, 0);
     load_k(t, t1, 1);
-    load_v(t, t0, 0);
+    load_v(t0, 0);
   }
   int nv0 = tile_valid(t0), nv1 = tile_valid(t1), nv2 = tile_valid(t2), nv3 = tile_valid(t3);
   float ks2 = load_ks(t2);
@@ -1247,7 +1254,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   // first operands of the sub-tile after (K rows at kbn) into pre.
   auto sub_tile = [&](i32x4 (&pk)[2][2], i32x4 (&pkn)[2][2], uint32_t kb, uint32_t vbo, uint32_t kbn,
                       i32x4 (&pre)[LA], int nvs, float ctn, bool live, auto loads_c, const char *lkb, uint32_t lkd,
-                      const char *lvb, uint32_t lvd, uint32_t lvrs) {
+                      const char *lvb, uint32_t lvd) {
     const float nbn[2] = {-fmaf(kI8MagicF, ctn, mref[0]), -fmaf(kI8MagicF, ctn, mref[1])};
     auto read_op = [&](int i) -> i32x4 {
       if (i < NQK) return lds_read(kb + i * 32);
@@ -1274,7 +1281,7 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
       if (loads)
 #pragma unroll
         for (int n = 0; n < NLD; ++n)
-          if (pl.l[n] == r) load_one(n, tab, lkb, lkd, lvb, lvd, lvrs);
+          if (pl.l[n] == r) load_one(n, tab, lkb, lkd, lvb, lvd);
       if (r == 2 * NQK + kGuardRegionOffset) {
         // first reads of the scores: at least 12 wait states after the last
         // score MFMA; naming them keeps every read below
@@ -1334,12 +1341,12 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
   for (;;) {
     // P of keys 0..31 of tile j; scores of keys 32..63 of tile j
     sub_tile(pkA, pkB, kro + b0 * KT + 32 * KRS, vro + vb * VT, kro + b1 * KT, pre, nv0 - 32, cq * ks0, true,
-             std::true_type{}, lkb, lkd, lvb, lvd, lvrs);
+             std::true_type{}, lkb, lkd, lvb, lvd);
     // P of keys 32..63 of tile j; scores of keys 0..31 of tile j+1 (after the
     // last tile they read a stale in-bounds buffer and are unused)
     const bool more = j + 1 < cnt;
     sub_tile(pkB, pkA, kro + b1 * KT, vro + vb * VT + 4 * 16, kro + b1 * KT + 32 * KRS, pre, nv1, cq * ks1, more,
-             std::false_type{}, lkb, lkd, lvb, lvd, lvrs);
+             std::false_type{}, lkb, lkd, lvb, lvd);
     if (!more) break;
     ++j;
     wait_vmem();
@@ -1357,7 +1364,10 @@ __global__ void __launch_bounds__(kWaves * 64) __attribute__((amdgpu_waves_per_e
     lkb = sk.kb + (int64_t)sk.t * (kBN * KROW);
     lkd = lds0 + b2 * KT;
     lvb = sv.vb + sv.t * (kBN * 2);
-    lvrs = sv.vrs2;
+    if (sv.vrs2 != lvrs) {  // the value loads moved to a segment with another row stride
+      lvrs = sv.vrs2;
+      write_vtab(lvrs);
+    }
     lvd = lds0 + 3 * KT + (vb ^ 1) * VT;
     ks2 = load_ks(sk);
     sv = sk;
