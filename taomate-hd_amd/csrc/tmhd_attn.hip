@@ -13,8 +13,8 @@
 //   keeps their query operands and fp32 output accumulators in AGPRs at fixed
 //   registers, the score chain starts (BF16: -m per half) at fixed VGPRs
 //   v[224:255], and the scores, probabilities and online-softmax state in
-//   the other VGPRs.  Fixed registers keep the
-//   compiler from moving these long-lived values around the loop.
+//   the other VGPRs.  Fixed registers keep the compiler from moving these
+//   long-lived values around the loop.
 //   Keys and values stream through LDS in 64-token tiles, triple-buffered
 //   (tile t in buffer t % 3) and loaded with global_load_lds_dwordx4 (no
 //   VGPR staging): K runs two tiles ahead of the tile being finished, V one.
@@ -974,10 +974,11 @@ constexpr bool plan8_valid(const SlotPlan8 &s, int nqk, int npv, int db, int nld
 }
 
 // S^T (+)= K Q^T for one 32-byte k-step, all in VGPRs; `first` starts the
-// chain at the inline constant 1/(2 pi) (bits 0x3E22F983).  Volatile, like every MFMA of this kernel: the hazard waits in
-// front of VALU reads of MFMA results (mfma_drain, the score guard) are
-// volatile asm too, and only volatile asm keeps its order relative to them (a
-// plain asm MFMA may be sunk below a drain that does not name its registers).
+// chain at the inline constant 1/(2 pi) (bits 0x3E22F983).  Volatile, like
+// every MFMA of this kernel: the hazard waits in front of VALU reads of MFMA
+// results (mfma_drain, the score guard) are volatile asm too, and only
+// volatile asm keeps its order relative to them (a plain asm MFMA may be sunk
+// below a drain that does not name its registers).
 __device__ __forceinline__ void qk_i8z(bool first, i32x16 &d, i32x4 k, const i32x4 &q) {
   if (first)
     asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, 0.15915494309189532" : "=&v"(d) : "v"(k), "v"(q));
